@@ -1,0 +1,82 @@
+// common.h -- internal helpers shared by the HIP sources of libgpt2amd.so (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "gpt2_kernels.h"
+#include "gpt2_kvcache.h"
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+namespace g2 {
+
+// Launch stream for every launcher (set by gpt2_set_stream).
+hipStream_t stream();
+
+// Record the first error since the last gpt2_last_error(); later ones are dropped.
+void set_error(int code, const char *what);
+// Codes >= 1000 are host-side argument errors; below that they are hipError_t values.
+enum { E_ARG = 1000, E_ALIGN = 1001, E_FORMAT = 1002, E_CAPACITY = 1003, E_STATE = 1004 };
+
+// Check the launch that was just enqueued.
+void check_launch(const char *what);
+
+// A decode step reads (token, pos) from immediates or, under graph replay, from a small
+// device-resident state {token, pos}.
+struct StepArg {
+    int token, pos;
+    const int *state;  // nullptr: use the immediates
+    __device__ __forceinline__ int tok() const { return state ? state[0] : token; }
+    __device__ __forceinline__ int p() const { return state ? state[1] : pos; }
+};
+
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+inline int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
+
+inline bool arg_fail(const char *what) {
+    set_error(E_ARG, what);
+    return true;
+}
+
+// Wave64 helpers -------------------------------------------------------------------------------
+// Sum over the 16 lanes of each DPP row (lanes 16r..16r+15); every lane receives the row sum.
+__device__ __forceinline__ float row16_sum(float v) {
+    // quad_perm [1,0,3,2] (xor 1), quad_perm [2,3,0,1] (xor 2), row_half_mirror, row_mirror
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, true));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return (float)__builtin_bit_cast(f16, h);
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+    return __builtin_bit_cast(uint16_t, (f16)f);   // v_cvt_f16_f32: round to nearest even
+}
+
+}  // namespace g2
+
+#define G2_HALF(p) reinterpret_cast<f16 *>(p)
+#define G2_CHALF(p) reinterpret_cast<const f16 *>(p)

@@ -1,0 +1,576 @@
+// engine.hip -- host side of the matmul path: backend table and dispatch, fp16 upload, scratch,
+// prefill forward, KV cache, the decode step and its hipGraph replay, and the two weight formats.
+//
+// Call order and data flow follow the reference host code (cuda/forward_cuda.cu, cuda/kvcache.cu,
+// cuda/kernels_quant.cu, model/weights.c); everything runs on the stream set by gpt2_set_stream.
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "common.h"
+
+namespace g2 {
+void gemv(uint16_t *C, const uint16_t *x, const void *W, const float *Ws, const uint16_t *bias, int N, int K, bool qw,
+          int cfg);
+void embed_one(uint16_t *x, const uint16_t *wte, const uint16_t *wpe, StepArg st);
+void kv_append(uint16_t *K, uint16_t *V, const uint16_t *qkv, StepArg st, int maxT);
+void attn_decode(uint16_t *att, const uint16_t *qkv, const uint16_t *K, const uint16_t *V, int maxT, StepArg st,
+                 int len_imm);
+void argmax_advance(const uint16_t *logits, int V, int *state, int *tokens, int max_pos);
+}  // namespace g2
+
+using namespace g2;
+
+// ============================================================================ backends
+// Composed exactly like the reference's (cuda/kernels_quant.cu:190-200, kvcache.cu:282-290): each
+// stage fills more slots.  All members are addresses of extern "C" functions, so the tables are
+// constant-initialized.  They exist in the host pass only (the device pass would otherwise treat
+// these const globals as __constant__ data referring to host functions).
+#if !defined(__HIP_DEVICE_COMPILE__)
+extern "C" const GPT2Backend GPT2_BACKEND_NAIVE = {
+    "naive", gpt2_embed, gpt2_layernorm, gpt2_matmul_naive, gpt2_attention_flash, gpt2_gelu, gpt2_add,
+    nullptr, nullptr, nullptr};
+extern "C" const GPT2Backend GPT2_BACKEND_TILED = {
+    "tiled", gpt2_embed, gpt2_layernorm, gpt2_matmul_tiled, gpt2_attention_flash, gpt2_gelu, gpt2_add,
+    nullptr, nullptr, nullptr};
+extern "C" const GPT2Backend GPT2_BACKEND_FLASH = {
+    "flash", gpt2_embed, gpt2_layernorm, gpt2_matmul_tiled, gpt2_attention_flash, gpt2_gelu, gpt2_add,
+    nullptr, nullptr, nullptr};
+extern "C" const GPT2Backend GPT2_BACKEND_INT8 = {
+    "int8", gpt2_embed, gpt2_layernorm, gpt2_matmul_tiled, gpt2_attention_flash, gpt2_gelu, gpt2_add,
+    gpt2_matmul_int8, gpt2_gemv_fp16, gpt2_gemv_int8};
+extern "C" const GPT2Backend GPT2_BACKEND_GEMV = {
+    "gemv", gpt2_embed, gpt2_layernorm, gpt2_matmul_tiled, gpt2_attention_flash, gpt2_gelu, gpt2_add,
+    nullptr, gpt2_gemv_fp16, nullptr};
+#endif
+
+extern "C" const GPT2Backend *gpt2_backend_by_name(const char *name) {
+    if (!name) return &GPT2_BACKEND_NAIVE;
+    if (!strcmp(name, "tiled")) return &GPT2_BACKEND_TILED;
+    if (!strcmp(name, "flash")) return &GPT2_BACKEND_FLASH;
+    if (!strcmp(name, "int8")) return &GPT2_BACKEND_INT8;
+    if (!strcmp(name, "gemv")) return &GPT2_BACKEND_GEMV;
+    return &GPT2_BACKEND_NAIVE;
+}
+
+extern "C" void gpt2_matmul_dispatch(const GPT2Backend *be, gpt2_half *C, const gpt2_half *A, const gpt2_half *Wh,
+                                     const GPT2QW *Wq, const gpt2_half *bias, int M, int N, int K) {
+    if (be->matmul_q && Wq && Wq->q) be->matmul_q(C, A, Wq->q, Wq->s, bias, M, N, K);
+    else be->matmul(C, A, Wh, bias, M, N, K);
+}
+
+extern "C" void gpt2_gemv_dispatch(const GPT2Backend *be, gpt2_half *C, const gpt2_half *A, const gpt2_half *Wh,
+                                   const GPT2QW *Wq, const gpt2_half *bias, int N, int K) {
+    if (be->gemv_q && Wq && Wq->q) be->gemv_q(C, A, Wq->q, Wq->s, bias, N, K);
+    else if (be->gemv) be->gemv(C, A, Wh, bias, N, K);
+    else gpt2_matmul_dispatch(be, C, A, Wh, Wq, bias, 1, N, K);
+}
+
+// ============================================================================ host fp32 weights
+static const int kMagicW = 0x47505432;  // 'GPT2'
+static const int kMagicQ = 0x38515047;  // 'GPQ8'
+
+extern "C" size_t gpt2_bind_weights(GPT2Weights *w, float *body) {
+    // tensor order of the file body (model/weights.c:44-55)
+    const size_t E = GPT2_N_EMBD, V = GPT2_VOCAB, CX = GPT2_N_CTX, Q = GPT2_QKV_DIM, F = GPT2_FFN_DIM;
+    float *c = body;
+    auto take = [&](size_t n) { float *p = c; c += n; return p; };
+    w->data = body;
+    w->n_floats = (size_t)GPT2_TOTAL_PARAMS;
+    w->wte = take(V * E);
+    w->wpe = take(CX * E);
+    for (int L = 0; L < GPT2_N_LAYER; ++L) {
+        GPT2Layer *l = &w->layers[L];
+        l->ln1_g = take(E); l->ln1_b = take(E);
+        l->qkv_w = take(Q * E); l->qkv_b = take(Q);
+        l->attn_proj_w = take(E * E); l->attn_proj_b = take(E);
+        l->ln2_g = take(E); l->ln2_b = take(E);
+        l->fc_w = take(F * E); l->fc_b = take(F);
+        l->proj_w = take(E * F); l->proj_b = take(E);
+    }
+    w->lnf_g = take(E);
+    w->lnf_b = take(E);
+    return (size_t)(c - body);
+}
+
+extern "C" int gpt2_load_weights(const char *path, GPT2Weights *w) {
+    memset(w, 0, sizeof(*w));
+    FILE *f = fopen(path, "rb");
+    if (!f) { fprintf(stderr, "[weights] cannot open %s\n", path); return 1; }
+    int32_t hdr[16];
+    if (fread(hdr, 4, 16, f) != 16) { fclose(f); fprintf(stderr, "[weights] short header\n"); return 2; }
+    if (hdr[0] != kMagicW || hdr[1] != 1) { fclose(f); fprintf(stderr, "[weights] bad magic/version\n"); return 3; }
+    if (hdr[2] != GPT2_N_LAYER || hdr[3] != GPT2_N_HEAD || hdr[4] != GPT2_N_EMBD || hdr[5] != GPT2_VOCAB ||
+        hdr[6] != GPT2_N_CTX || hdr[7] != GPT2_FFN_DIM || hdr[8] != GPT2_QKV_DIM) {
+        fclose(f);
+        fprintf(stderr, "[weights] dims mismatch\n");
+        return 4;
+    }
+    if (hdr[9] != 0) { fclose(f); fprintf(stderr, "[weights] dtype != fp32\n"); return 5; }
+    const size_t n = (size_t)GPT2_TOTAL_PARAMS;
+    float *body = (float *)malloc(n * sizeof(float));
+    if (!body) { fclose(f); return 6; }
+    const size_t got = fread(body, sizeof(float), n, f);
+    const long cur = ftell(f);
+    fseek(f, 0, SEEK_END);
+    const long extra = ftell(f) - cur;
+    fclose(f);
+    if (got != n) { free(body); fprintf(stderr, "[weights] short body\n"); return 7; }
+    if (extra != 0) { free(body); fprintf(stderr, "[weights] %ld trailing bytes\n", extra); return 8; }
+    if (gpt2_bind_weights(w, body) != n) { free(body); memset(w, 0, sizeof(*w)); return 9; }
+    return 0;
+}
+
+extern "C" void gpt2_free_weights(GPT2Weights *w) {
+    if (w && w->data) {
+        free(w->data);
+        w->data = nullptr;
+    }
+}
+
+// ============================================================================ fp16 upload
+extern "C" void gpt2_upload_fp16(const GPT2Weights *cpu, GPT2WeightsGPU *gpu) {
+    memset(gpu, 0, sizeof(*gpu));
+    if (!cpu || !cpu->data || cpu->n_floats == 0) { arg_fail("gpt2_upload_fp16: no host body"); return; }
+    const size_t n = cpu->n_floats;
+    uint16_t *dst = (uint16_t *)gpt2_dmalloc(n * 2);
+    if (!dst) return;
+    // Stage the fp32 body through one bounded device buffer and convert on the GPU.
+    const size_t chunk = (size_t)32 << 20;   // floats per pass (128 MiB)
+    float *stage = (float *)gpt2_dmalloc((n < chunk ? n : chunk) * 4);
+    if (!stage) { gpt2_dfree(dst); return; }
+    for (size_t off = 0; off < n; off += chunk) {
+        const size_t m = (n - off < chunk) ? n - off : chunk;
+        if (gpt2_h2d(stage, cpu->data + off, m * 4)) break;
+        gpt2_f32_to_f16(dst + off, stage, m);
+        gpt2_sync();
+    }
+    gpt2_dfree(stage);
+    gpu->data = dst;
+    gpu->n = n;
+    auto OFF = [&](const float *p) { return dst + (p - cpu->data); };
+    gpu->wte = OFF(cpu->wte);
+    gpu->wpe = OFF(cpu->wpe);
+    for (int L = 0; L < GPT2_N_LAYER; ++L) {
+        const GPT2Layer *c = &cpu->layers[L];
+        GPT2LayerGPU *g = &gpu->layers[L];
+        g->ln1_g = OFF(c->ln1_g); g->ln1_b = OFF(c->ln1_b);
+        g->qkv_w = OFF(c->qkv_w); g->qkv_b = OFF(c->qkv_b);
+        g->attn_proj_w = OFF(c->attn_proj_w); g->attn_proj_b = OFF(c->attn_proj_b);
+        g->ln2_g = OFF(c->ln2_g); g->ln2_b = OFF(c->ln2_b);
+        g->fc_w = OFF(c->fc_w); g->fc_b = OFF(c->fc_b);
+        g->proj_w = OFF(c->proj_w); g->proj_b = OFF(c->proj_b);
+    }
+    gpu->lnf_g = OFF(cpu->lnf_g);
+    gpu->lnf_b = OFF(cpu->lnf_b);
+    gpu->q = nullptr;
+}
+
+extern "C" void gpt2_free_gpu(GPT2WeightsGPU *g) {
+    if (g && g->data) {
+        gpt2_dfree(g->data);
+        g->data = nullptr;
+    }
+}
+
+extern "C" void gpt2_scratch_alloc(GPT2ScratchGPU *s, int maxT) {
+    memset(s, 0, sizeof(*s));
+    if (maxT <= 0) { arg_fail("gpt2_scratch_alloc: maxT <= 0"); return; }
+    s->maxT = maxT;
+    const size_t E = GPT2_N_EMBD, Q = GPT2_QKV_DIM, F = GPT2_FFN_DIM, T = (size_t)maxT;
+    s->x = (gpt2_half *)gpt2_dmalloc(T * E * 2);
+    s->ln = (gpt2_half *)gpt2_dmalloc(T * E * 2);
+    s->qkv = (gpt2_half *)gpt2_dmalloc(T * Q * 2);
+    s->att = (gpt2_half *)gpt2_dmalloc(T * E * 2);
+    s->ao = (gpt2_half *)gpt2_dmalloc(T * E * 2);
+    s->fc = (gpt2_half *)gpt2_dmalloc(T * F * 2);
+    s->ff = (gpt2_half *)gpt2_dmalloc(T * E * 2);
+}
+
+extern "C" void gpt2_scratch_free(GPT2ScratchGPU *s) {
+    gpt2_dfree(s->x); gpt2_dfree(s->ln); gpt2_dfree(s->qkv); gpt2_dfree(s->att);
+    gpt2_dfree(s->ao); gpt2_dfree(s->fc); gpt2_dfree(s->ff);
+    memset(s, 0, sizeof(*s));
+}
+
+// ============================================================================ prefill forward
+static void capcpy(gpt2_half *dst, const gpt2_half *src, size_t n) { gpt2_d2d(dst, src, n * 2); }
+
+extern "C" void gpt2_forward_cuda(const GPT2Backend *be, const GPT2WeightsGPU *w, const int *d_ids, int T,
+                                  GPT2ScratchGPU *s, GPT2CapsGPU *caps) {
+    if (!be || !w || !w->data || !s || !d_ids || T <= 0 || T > s->maxT || T > GPT2_N_CTX) {
+        arg_fail("gpt2_forward_cuda: bad arguments (T must be in [1, min(maxT, 1024)])");
+        return;
+    }
+    const int E = GPT2_N_EMBD, Q = GPT2_QKV_DIM, F = GPT2_FFN_DIM, V = GPT2_VOCAB, H = GPT2_N_HEAD, D = GPT2_HEAD_DIM;
+    const GPT2QWeightsGPU *qw = w->q;
+    GPT2KVCache *kv = caps ? caps->kv : nullptr;
+    if (kv && T > kv->maxT) { arg_fail("gpt2_forward_cuda: T exceeds the KV cache"); return; }
+
+    be->embed(s->x, w->wte, w->wpe, d_ids, T, E);
+    if (caps && caps->embed) capcpy(caps->embed, s->x, (size_t)T * E);
+    for (int L = 0; L < GPT2_N_LAYER; ++L) {
+        const GPT2LayerGPU *ly = &w->layers[L];
+        const GPT2QLayerGPU *qy = qw ? &qw->layers[L] : nullptr;
+        be->layernorm(s->ln, s->x, ly->ln1_g, ly->ln1_b, T, E);
+        gpt2_matmul_dispatch(be, s->qkv, s->ln, ly->qkv_w, qy ? &qy->qkv_w : nullptr, ly->qkv_b, T, Q, E);
+        if (kv) gpt2_kv_scatter_prefill(kv, L, s->qkv, T);
+        be->attention(s->att, s->qkv, T, E, H, D);
+        gpt2_matmul_dispatch(be, s->ao, s->att, ly->attn_proj_w, qy ? &qy->attn_proj_w : nullptr, ly->attn_proj_b, T, E, E);
+        be->add(s->x, s->ao, (size_t)T * E);
+        be->layernorm(s->ln, s->x, ly->ln2_g, ly->ln2_b, T, E);
+        gpt2_matmul_dispatch(be, s->fc, s->ln, ly->fc_w, qy ? &qy->fc_w : nullptr, ly->fc_b, T, F, E);
+        be->gelu(s->fc, (size_t)T * F);
+        gpt2_matmul_dispatch(be, s->ff, s->fc, ly->proj_w, qy ? &qy->proj_w : nullptr, ly->proj_b, T, E, F);
+        be->add(s->x, s->ff, (size_t)T * E);
+        if (caps && caps->blocks) capcpy(caps->blocks + (size_t)L * T * E, s->x, (size_t)T * E);
+    }
+    be->layernorm(s->ln, s->x, w->lnf_g, w->lnf_b, T, E);
+    if (caps && caps->final_ln) capcpy(caps->final_ln, s->ln, (size_t)T * E);
+    if (caps && caps->logits) {
+        const GPT2QW *qh = qw ? &qw->wte : nullptr;
+        if (caps->logits_all) gpt2_matmul_dispatch(be, caps->logits, s->ln, w->wte, qh, nullptr, T, V, E);
+        else gpt2_matmul_dispatch(be, caps->logits, s->ln + (size_t)(T - 1) * E, w->wte, qh, nullptr, 1, V, E);
+    }
+}
+
+// ============================================================================ KV cache
+extern "C" int gpt2_kv_alloc(GPT2KVCache *kv, int maxT) {
+    memset(kv, 0, sizeof(*kv));
+    if (maxT <= 0 || maxT > GPT2_N_CTX) { arg_fail("gpt2_kv_alloc: maxT out of range"); return 1; }
+    kv->maxT = maxT;
+    kv->nLayer = GPT2_N_LAYER;
+    kv->nHead = GPT2_N_HEAD;
+    kv->headDim = GPT2_HEAD_DIM;
+    kv->bytes = (size_t)2 * GPT2_N_LAYER * GPT2_N_HEAD * maxT * GPT2_HEAD_DIM * 2;
+    size_t freeB = 0, totB = 0;
+    if (hipMemGetInfo(&freeB, &totB) != hipSuccess) return 1;
+    if (kv->bytes + ((size_t)64 << 20) > freeB) return 1;   // keep 64 MiB of headroom (cuda/kvcache.cu:32-37)
+    kv->data = (gpt2_half *)gpt2_dmalloc(kv->bytes);
+    return kv->data ? 0 : 1;
+}
+
+extern "C" void gpt2_kv_free(GPT2KVCache *kv) {
+    if (kv && kv->data) {
+        gpt2_dfree(kv->data);
+        kv->data = nullptr;
+    }
+}
+
+extern "C" void gpt2_kv_reset(GPT2KVCache *kv) {
+    if (kv) kv->len = 0;
+}
+
+extern "C" double gpt2_kv_step_bytes(const GPT2KVCache *kv, int len) {
+    return 2.0 * kv->nLayer * kv->nHead * (double)len * kv->headDim * 2.0;
+}
+
+// ============================================================================ decode step
+// One token (cuda/kvcache.cu:233-269).  With st.state set, token/pos come from device memory and
+// the step ends with the greedy argmax that advances that state (the graph-replayed form).
+static void decode_step(const GPT2Backend *be, const GPT2WeightsGPU *w, GPT2KVCache *kv, StepArg st,
+                        GPT2ScratchGPU *s, gpt2_half *logits, gpt2_half *caps, int *state, int *tokens) {
+    const int E = GPT2_N_EMBD, Q = GPT2_QKV_DIM, F = GPT2_FFN_DIM, V = GPT2_VOCAB;
+    const GPT2QWeightsGPU *qw = w->q;
+    const int len_imm = st.state ? 0 : st.pos + 1;
+    embed_one(s->x, w->wte, w->wpe, st);
+    if (caps) capcpy(caps + (size_t)(GPT2_N_LAYER + 1) * E, s->x, E);
+    for (int L = 0; L < GPT2_N_LAYER; ++L) {
+        const GPT2LayerGPU *ly = &w->layers[L];
+        const GPT2QLayerGPU *qy = qw ? &qw->layers[L] : nullptr;
+        be->layernorm(s->ln, s->x, ly->ln1_g, ly->ln1_b, 1, E);
+        gpt2_gemv_dispatch(be, s->qkv, s->ln, ly->qkv_w, qy ? &qy->qkv_w : nullptr, ly->qkv_b, Q, E);
+        kv_append(gpt2_kv_K(kv, L), gpt2_kv_V(kv, L), s->qkv, st, kv->maxT);
+        attn_decode(s->att, s->qkv, gpt2_kv_K(kv, L), gpt2_kv_V(kv, L), kv->maxT, st, len_imm);
+        gpt2_gemv_dispatch(be, s->ao, s->att, ly->attn_proj_w, qy ? &qy->attn_proj_w : nullptr, ly->attn_proj_b, E, E);
+        be->add(s->x, s->ao, (size_t)E);
+        be->layernorm(s->ln, s->x, ly->ln2_g, ly->ln2_b, 1, E);
+        gpt2_gemv_dispatch(be, s->fc, s->ln, ly->fc_w, qy ? &qy->fc_w : nullptr, ly->fc_b, F, E);
+        be->gelu(s->fc, (size_t)F);
+        gpt2_gemv_dispatch(be, s->ff, s->fc, ly->proj_w, qy ? &qy->proj_w : nullptr, ly->proj_b, E, F);
+        be->add(s->x, s->ff, (size_t)E);
+        if (caps) capcpy(caps + (size_t)L * E, s->x, E);
+    }
+    be->layernorm(s->ln, s->x, w->lnf_g, w->lnf_b, 1, E);
+    if (caps) capcpy(caps + (size_t)GPT2_N_LAYER * E, s->ln, E);
+    if (logits) gpt2_gemv_dispatch(be, logits, s->ln, w->wte, qw ? &qw->wte : nullptr, nullptr, V, E);
+    if (state) argmax_advance(logits, V, state, tokens, kv->maxT);
+}
+
+extern "C" void gpt2_decode_step_cuda(const GPT2Backend *be, const GPT2WeightsGPU *w, GPT2KVCache *kv, int token,
+                                      int pos, GPT2ScratchGPU *s, gpt2_half *logits, gpt2_half *caps_blocks) {
+    if (!be || !w || !w->data || !kv || !kv->data || !s || s->maxT < 1) { arg_fail("gpt2_decode_step_cuda: null argument"); return; }
+    if (pos < 0 || pos >= kv->maxT || pos > kv->len || token < 0 || token >= GPT2_VOCAB) {
+        arg_fail("gpt2_decode_step_cuda: need 0 <= pos <= kv->len, pos < maxT, token < vocab");
+        return;
+    }
+    decode_step(be, w, kv, StepArg{token, pos, nullptr}, s, logits, caps_blocks, nullptr, nullptr);
+    kv->len = pos + 1;
+}
+
+extern "C" void gpt2_prefill_fill_cache(const GPT2Backend *be, const GPT2WeightsGPU *w, GPT2KVCache *kv,
+                                        const int *d_ids, int T, GPT2ScratchGPU *s, GPT2CapsGPU *caps) {
+    GPT2CapsGPU c;
+    if (caps) c = *caps;
+    else memset(&c, 0, sizeof(c));
+    c.kv = kv;
+    const int before = gpt2_last_error();
+    gpt2_forward_cuda(be, w, d_ids, T, s, &c);
+    const int err = gpt2_last_error();
+    if (before) set_error(before, "before gpt2_prefill_fill_cache");
+    if (err) set_error(err, "gpt2_prefill_fill_cache");
+    else kv->len = T;
+}
+
+// ============================================================================ graph replay
+struct GPT2DecodeGraph {
+    hipStream_t stream;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    int *state;       // device {token, pos}
+    GPT2KVCache *kv;
+    int host_pos;     // position the next replay consumes, tracked on the host
+};
+
+extern "C" GPT2DecodeGraph *gpt2_decode_graph_create(const GPT2Backend *be, const GPT2WeightsGPU *w, GPT2KVCache *kv,
+                                                     GPT2ScratchGPU *s, gpt2_half *logits, int *tokens) {
+    if (!be || !w || !w->data || !kv || !kv->data || !s || !logits) { arg_fail("gpt2_decode_graph_create: null argument"); return nullptr; }
+    GPT2DecodeGraph *g = new GPT2DecodeGraph();
+    g->kv = kv;
+    g->host_pos = kv->len;
+    if (hipStreamCreate(&g->stream) != hipSuccess) { delete g; set_error(E_STATE, "hipStreamCreate"); return nullptr; }
+    g->state = (int *)gpt2_dmalloc(2 * sizeof(int));
+    const int init[2] = {0, kv->len};
+    hipMemcpy(g->state, init, sizeof(init), hipMemcpyHostToDevice);
+
+    hipStream_t prev = stream();
+    gpt2_set_stream(g->stream);
+    hipError_t e = hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal);
+    if (e == hipSuccess) {
+        decode_step(be, w, kv, StepArg{0, 0, g->state}, s, logits, nullptr, g->state, tokens);
+        e = hipStreamEndCapture(g->stream, &g->graph);
+    }
+    gpt2_set_stream(prev);
+    if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        set_error((int)e, "decode graph capture/instantiate");
+        hipStreamDestroy(g->stream);
+        gpt2_dfree(g->state);
+        delete g;
+        return nullptr;
+    }
+    return g;
+}
+
+extern "C" int gpt2_decode_graph_set(GPT2DecodeGraph *g, int token, int pos) {
+    if (!g || token < 0 || token >= GPT2_VOCAB || pos < 0 || pos >= g->kv->maxT) { set_error(E_ARG, "gpt2_decode_graph_set"); return 1; }
+    const int st[2] = {token, pos};
+    hipError_t e = hipMemcpyAsync(g->state, st, sizeof(st), hipMemcpyHostToDevice, g->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g->stream);
+    if (e != hipSuccess) { set_error((int)e, "gpt2_decode_graph_set"); return (int)e; }
+    g->host_pos = pos;
+    return 0;
+}
+
+extern "C" int gpt2_decode_graph_run(GPT2DecodeGraph *g, int steps) {
+    if (!g || steps < 0) { set_error(E_ARG, "gpt2_decode_graph_run"); return 1; }
+    if (g->host_pos + steps > g->kv->maxT) { set_error(E_CAPACITY, "gpt2_decode_graph_run: past the cache"); return 1; }
+    for (int i = 0; i < steps; ++i) {
+        hipError_t e = hipGraphLaunch(g->exec, g->stream);
+        if (e != hipSuccess) { set_error((int)e, "hipGraphLaunch"); return (int)e; }
+    }
+    g->host_pos += steps;
+    return 0;
+}
+
+extern "C" int gpt2_decode_graph_sync(GPT2DecodeGraph *g, int *token, int *pos) {
+    if (!g) return 1;
+    int st[2];
+    hipError_t e = hipMemcpyAsync(st, g->state, sizeof(st), hipMemcpyDeviceToHost, g->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g->stream);
+    if (e != hipSuccess) { set_error((int)e, "gpt2_decode_graph_sync"); return (int)e; }
+    if (token) *token = st[0];
+    if (pos) *pos = st[1];
+    g->kv->len = st[1];
+    g->host_pos = st[1];
+    return 0;
+}
+
+extern "C" void gpt2_decode_graph_destroy(GPT2DecodeGraph *g) {
+    if (!g) return;
+    hipStreamSynchronize(g->stream);
+    hipGraphExecDestroy(g->exec);
+    hipGraphDestroy(g->graph);
+    hipStreamDestroy(g->stream);
+    gpt2_dfree(g->state);
+    delete g;
+}
+
+// ============================================================================ INT8 weights
+namespace {
+const int kNQ = 1 + 4 * GPT2_N_LAYER;
+
+struct QShape { int N, K; };
+
+void q_shapes(QShape *sh) {
+    sh[0] = {GPT2_VOCAB, GPT2_N_EMBD};
+    for (int L = 0; L < GPT2_N_LAYER; ++L) {
+        sh[1 + 4 * L + 0] = {GPT2_QKV_DIM, GPT2_N_EMBD};
+        sh[1 + 4 * L + 1] = {GPT2_N_EMBD, GPT2_N_EMBD};
+        sh[1 + 4 * L + 2] = {GPT2_FFN_DIM, GPT2_N_EMBD};
+        sh[1 + 4 * L + 3] = {GPT2_N_EMBD, GPT2_FFN_DIM};
+    }
+}
+
+void q_slots(GPT2QWeightsGPU *q, GPT2QW **dst) {
+    dst[0] = &q->wte;
+    for (int L = 0; L < GPT2_N_LAYER; ++L) {
+        dst[1 + 4 * L + 0] = &q->layers[L].qkv_w;
+        dst[1 + 4 * L + 1] = &q->layers[L].attn_proj_w;
+        dst[1 + 4 * L + 2] = &q->layers[L].fc_w;
+        dst[1 + 4 * L + 3] = &q->layers[L].proj_w;
+    }
+}
+
+const gpt2_half *fp16_tensor(const GPT2WeightsGPU *w, int i) {
+    if (i == 0) return w->wte;
+    const GPT2LayerGPU &l = w->layers[(i - 1) / 4];
+    switch ((i - 1) % 4) {
+        case 0: return l.qkv_w;
+        case 1: return l.attn_proj_w;
+        case 2: return l.fc_w;
+        default: return l.proj_w;
+    }
+}
+
+// Point the GPT2QW views into the arenas; flag 0 leaves q = NULL (fp16 fallback for that tensor).
+void q_attach(GPT2QWeightsGPU *q, const int *flag) {
+    QShape sh[kNQ];
+    q_shapes(sh);
+    GPT2QW *dst[kNQ];
+    q_slots(q, dst);
+    size_t oq = 0, os = 0, kept = 0;
+    for (int i = 0; i < kNQ; ++i) {
+        if (!flag[i]) {
+            dst[i]->q = nullptr;
+            dst[i]->s = nullptr;
+            kept += (size_t)sh[i].N * sh[i].K;
+            continue;
+        }
+        dst[i]->q = q->qdata + oq;
+        dst[i]->s = q->sdata + os;
+        oq += (size_t)sh[i].N * sh[i].K;
+        os += sh[i].N;
+    }
+    q->streamed_bytes = q->nq + q->ns * 4 + kept * 2;
+}
+}  // namespace
+
+extern "C" void gpt2_quant_free(GPT2QWeightsGPU *q) {
+    if (!q) return;
+    gpt2_dfree(q->qdata);
+    gpt2_dfree(q->sdata);
+    q->qdata = nullptr;
+    q->sdata = nullptr;
+}
+
+extern "C" int gpt2_quant_build(GPT2WeightsGPU *gpu, GPT2QWeightsGPU *q, const int *keep) {
+    memset(q, 0, sizeof(*q));
+    if (!gpu || !gpu->data) { arg_fail("gpt2_quant_build: no fp16 weights"); return 1; }
+    int flag[kNQ];
+    for (int i = 0; i < kNQ; ++i) flag[i] = keep ? !keep[i] : (i != 0);
+    QShape sh[kNQ];
+    q_shapes(sh);
+    for (int i = 0; i < kNQ; ++i)
+        if (flag[i]) { q->nq += (size_t)sh[i].N * sh[i].K; q->ns += sh[i].N; }
+    q->qdata = (int8_t *)gpt2_dmalloc(q->nq ? q->nq : 1);
+    q->sdata = (float *)gpt2_dmalloc((q->ns ? q->ns : 1) * 4);
+    if (!q->qdata || !q->sdata) { gpt2_quant_free(q); return 1; }
+    q_attach(q, flag);
+    GPT2QW *dst[kNQ];
+    q_slots(q, dst);
+    for (int i = 0; i < kNQ; ++i)
+        if (flag[i]) gpt2_quantize_rows((int8_t *)dst[i]->q, (float *)dst[i]->s, fp16_tensor(gpu, i), sh[i].N, sh[i].K);
+    if (gpt2_sync()) { gpt2_quant_free(q); return 1; }
+    gpu->q = q;
+    return 0;
+}
+
+extern "C" int gpt2_quant_load_upload(const char *path, GPT2WeightsGPU *gpu, GPT2QWeightsGPU *q) {
+    memset(q, 0, sizeof(*q));
+    FILE *f = fopen(path, "rb");
+    if (!f) { fprintf(stderr, "[quant] cannot open %s\n", path); return 1; }
+    int32_t hdr[16];
+    int flag[kNQ];
+    auto fail = [&](const char *why) { fprintf(stderr, "[quant] %s\n", why); fclose(f); return 1; };
+    if (fread(hdr, 4, 16, f) != 16) return fail("short header");
+    if (hdr[0] != kMagicQ) return fail("bad magic");
+    if (hdr[1] != 2) return fail("version != 2");
+    if (hdr[2] != GPT2_N_LAYER || hdr[3] != GPT2_N_EMBD || hdr[4] != GPT2_VOCAB || hdr[5] != GPT2_FFN_DIM ||
+        hdr[6] != GPT2_QKV_DIM || hdr[7] != kNQ)
+        return fail("dim mismatch");
+    if (fread(flag, 4, kNQ, f) != (size_t)kNQ) return fail("short flags");
+    QShape sh[kNQ];
+    q_shapes(sh);
+    for (int i = 0; i < kNQ; ++i)
+        if (flag[i]) { q->nq += (size_t)sh[i].N * sh[i].K; q->ns += sh[i].N; }
+    std::vector<int8_t> hq(q->nq ? q->nq : 1);
+    std::vector<float> hs(q->ns ? q->ns : 1);
+    size_t oq = 0, os = 0;
+    for (int i = 0; i < kNQ; ++i) {
+        if (!flag[i]) continue;
+        const size_t n = (size_t)sh[i].N * sh[i].K;
+        if (fread(hq.data() + oq, 1, n, f) != n) return fail("short q");
+        if (fread(hs.data() + os, 4, sh[i].N, f) != (size_t)sh[i].N) return fail("short s");
+        oq += n;
+        os += sh[i].N;
+    }
+    const long cur = ftell(f);
+    fseek(f, 0, SEEK_END);
+    const long extra = ftell(f) - cur;
+    fclose(f);
+    if (extra != 0) { fprintf(stderr, "[quant] %ld trailing bytes\n", extra); return 1; }
+    q->qdata = (int8_t *)gpt2_dmalloc(q->nq ? q->nq : 1);
+    q->sdata = (float *)gpt2_dmalloc((q->ns ? q->ns : 1) * 4);
+    if (!q->qdata || !q->sdata) { gpt2_quant_free(q); return 1; }
+    if (gpt2_h2d(q->qdata, hq.data(), q->nq) || gpt2_h2d(q->sdata, hs.data(), q->ns * 4)) { gpt2_quant_free(q); return 1; }
+    int fl[kNQ];
+    for (int i = 0; i < kNQ; ++i) fl[i] = flag[i] != 0;
+    q_attach(q, fl);
+    if (gpu) gpu->q = q;
+    return 0;
+}
+
+extern "C" int gpt2_quant_write_file(const char *path, const GPT2QWeightsGPU *q, const int *keep) {
+    if (!q || !path) return 1;
+    int flag[kNQ];
+    QShape sh[kNQ];
+    q_shapes(sh);
+    GPT2QW *dst[kNQ];
+    q_slots(const_cast<GPT2QWeightsGPU *>(q), dst);
+    for (int i = 0; i < kNQ; ++i) flag[i] = dst[i]->q != nullptr;
+    if (keep)
+        for (int i = 0; i < kNQ; ++i)
+            if (keep[i] && flag[i]) return 1;   // asked to keep a tensor that is quantized
+    FILE *f = fopen(path, "wb");
+    if (!f) return 1;
+    int32_t hdr[16] = {kMagicQ, 2, GPT2_N_LAYER, GPT2_N_EMBD, GPT2_VOCAB, GPT2_FFN_DIM, GPT2_QKV_DIM, kNQ};
+    bool ok = fwrite(hdr, 4, 16, f) == 16 && fwrite(flag, 4, kNQ, f) == (size_t)kNQ;
+    for (int i = 0; ok && i < kNQ; ++i) {
+        if (!flag[i]) continue;
+        const size_t n = (size_t)sh[i].N * sh[i].K;
+        std::vector<int8_t> hq(n);
+        std::vector<float> hs(sh[i].N);
+        ok = !gpt2_d2h(hq.data(), dst[i]->q, n) && !gpt2_d2h(hs.data(), dst[i]->s, (size_t)sh[i].N * 4) &&
+             fwrite(hq.data(), 1, n, f) == n && fwrite(hs.data(), 4, sh[i].N, f) == (size_t)sh[i].N;
+    }
+    return (fclose(f) == 0 && ok) ? 0 : 1;
+}
+
+extern "C" int gpt2_quant_attach_if_needed(const GPT2Backend *be, GPT2WeightsGPU *gpu, GPT2QWeightsGPU *q) {
+    memset(q, 0, sizeof(*q));
+    if (!be->matmul_q) return 0;
+    const char *p = getenv("GPT2_INT8_WEIGHTS");
+    return gpt2_quant_load_upload(p ? p : "weights/gpt2_124m_int8_kt.bin", gpu, q);
+}

@@ -1,0 +1,365 @@
+// gemm.hip -- prefill GEMMs for gfx950: C[M,N] = A[M,K] . W[N,K]^T (+bias), fp16 in, fp32 acc.
+//
+// Replaces the reference's 16x16 CUDA-core tiled GEMM (cuda/kernels_tiled.cu:24-53) and its INT8
+// twin (cuda/kernels_quant.cu:38-67).  Design, MI355X-first:
+//   * v_mfma_f32_16x16x32_f16: W rows feed the MFMA "A" operand and activation rows the "B"
+//     operand, so the accumulator holds D[n][m] = C[m][n] and each lane owns four consecutive n of
+//     one output row m: the epilogue writes 8-byte vectors into row-major C.
+//   * Both operands are K-contiguous, so a 16-byte global load is 8 consecutive k of one row.  Tiles
+//     are staged through LDS, double-buffered (one barrier per k-tile), with the 16-byte chunk index
+//     XOR-swizzled by row so that the ds_read_b128 fragment reads and the ds_write_b128 stores hit
+//     distinct banks.
+//   * The MFMA k-lane mapping only has to agree between the two operands (a dot product is order
+//     free), so each lane group reads 8 consecutive k of its row for both A and B.
+//   * INT8 weights (weight-only scheme) are converted to fp16 while staging: |q| <= 127 is exact in
+//     fp16 and the int8 x fp16 products are exact in fp32, so the MFMA path is the fp16 one; the
+//     per-row scale is applied once in the epilogue, then the bias (cuda/kernels_quant.cu:56-59).
+//   * Work-group -> tile mapping is XCD-aware: consecutive work-groups go round robin over the 8
+//     XCDs, so each XCD is given one contiguous run of tiles (n-major, m fastest), and the W tiles it
+//     reads stay in its own L2.
+// Shapes or pointers the MFMA path cannot take (K % 8 != 0, or unaligned rows) run k_gemm_generic.
+#include <cstdlib>
+#include <cstring>
+
+#include "common.h"
+
+namespace g2 {
+
+// 16-byte chunk swizzle inside an LDS row of CH chunks (CH = 4 or 8).
+template <int CH>
+__device__ __forceinline__ int swz(int row, int c) {
+    if constexpr (CH == 8) return c ^ (row & 7);
+    else return c ^ ((row >> 1) & 3);
+}
+
+// Sign-exact int8 -> fp16 for four packed bytes: (b ^ 0x80) is b + 128 in [1, 255]; the half with
+// bits 0x6400 | u is 1024 + u; subtracting 1152 leaves b.  Returns two f16x2 words (lo, hi).
+__device__ __forceinline__ void i8x4_to_f16x4(uint32_t w, uint32_t &lo, uint32_t &hi) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x05010400u);
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x07030602u);
+    const f16x2 bias = {(f16)-1152.0f, (f16)-1152.0f};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, a) + bias);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, b) + bias);
+}
+
+// Map the linear work-group id onto a tile id so that each XCD owns a contiguous tile range.
+__device__ __forceinline__ int xcd_tile(int bid, int ntiles) {
+    const int xcd = bid & 7, slot = bid >> 3;
+    const int per = ntiles >> 3, rem = ntiles & 7;
+    return xcd * per + (xcd < rem ? xcd : rem) + slot;
+}
+
+template <int BN, int BM, int BK, int WN, int WM, bool QW>
+__global__ __launch_bounds__(256) void k_gemm_mfma(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
+                                                   const void *__restrict__ Wv, const float *__restrict__ Ws,
+                                                   const uint16_t *__restrict__ bias, int M, int N, int K,
+                                                   int tiles_m, int ntiles, int vec_store) {
+    static_assert(WN * WM == 4, "four waves per work-group");
+    constexpr int CH = BK / 8;               // 16-byte chunks per LDS row
+    constexpr int WTN = BN / WN, WTM = BM / WM;  // wave tile
+    constexpr int TN = WTN / 16, TM = WTM / 16;
+    constexpr int GA = BM * CH;                    // 16-byte A chunks per k-tile
+    constexpr int GW = QW ? BN * CH / 2 : BN * CH; // 16-byte W chunks per k-tile (int8: 16 k each)
+    constexpr int NLA = (GA + 255) / 256, NLW = (GW + 255) / 256;
+
+    __shared__ __attribute__((aligned(16))) f16x8 sW[2][BN * CH];
+    __shared__ __attribute__((aligned(16))) f16x8 sA[2][BM * CH];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tile = xcd_tile(blockIdx.x, ntiles);
+    const int n0 = (tile / tiles_m) * BN, m0 = (tile % tiles_m) * BM;
+    const int wn0 = (wave / WM) * WTN, wm0 = (wave % WM) * WTM;
+    const int nk = (K + BK - 1) / BK;
+
+    const f16x8 zero8 = {};
+    f16x8 ra[NLA];
+    i32x4 rw[NLW];
+
+    auto gload = [&](int kt) {
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int i = 0; i < NLA; ++i) {
+            const int id = tid + 256 * i, row = id / CH, c = id % CH;
+            if (GA % 256 != 0 && id >= GA) break;
+            const int m = m0 + row, k = k0 + c * 8;
+            ra[i] = (m < M && k < K) ? *reinterpret_cast<const f16x8 *>(A + (size_t)m * K + k) : zero8;
+        }
+#pragma unroll
+        for (int i = 0; i < NLW; ++i) {
+            const int id = tid + 256 * i;
+            if (GW % 256 != 0 && id >= GW) break;
+            if constexpr (QW) {
+                constexpr int CQ = CH / 2;   // 16-byte int8 chunks per row
+                const int row = id / CQ, c = id % CQ;
+                const int n = n0 + row, k = k0 + c * 16;
+                const int8_t *W = reinterpret_cast<const int8_t *>(Wv);
+                rw[i] = (n < N && k < K) ? *reinterpret_cast<const i32x4 *>(W + (size_t)n * K + k) : i32x4{0, 0, 0, 0};
+            } else {
+                const int row = id / CH, c = id % CH;
+                const int n = n0 + row, k = k0 + c * 8;
+                const uint16_t *W = reinterpret_cast<const uint16_t *>(Wv);
+                rw[i] = (n < N && k < K) ? *reinterpret_cast<const i32x4 *>(W + (size_t)n * K + k) : i32x4{0, 0, 0, 0};
+            }
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < NLA; ++i) {
+            const int id = tid + 256 * i, row = id / CH, c = id % CH;
+            if (GA % 256 != 0 && id >= GA) break;
+            sA[buf][row * CH + swz<CH>(row, c)] = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < NLW; ++i) {
+            const int id = tid + 256 * i;
+            if (GW % 256 != 0 && id >= GW) break;
+            if constexpr (QW) {
+                constexpr int CQ = CH / 2;
+                const int row = id / CQ, c = id % CQ;
+                uint32_t h[8];
+                i8x4_to_f16x4((uint32_t)rw[i].x, h[0], h[1]);
+                i8x4_to_f16x4((uint32_t)rw[i].y, h[2], h[3]);
+                i8x4_to_f16x4((uint32_t)rw[i].z, h[4], h[5]);
+                i8x4_to_f16x4((uint32_t)rw[i].w, h[6], h[7]);
+                const i32x4 lo = {(int)h[0], (int)h[1], (int)h[2], (int)h[3]};
+                const i32x4 hi = {(int)h[4], (int)h[5], (int)h[6], (int)h[7]};
+                sW[buf][row * CH + swz<CH>(row, 2 * c)] = __builtin_bit_cast(f16x8, lo);
+                sW[buf][row * CH + swz<CH>(row, 2 * c + 1)] = __builtin_bit_cast(f16x8, hi);
+            } else {
+                const int row = id / CH, c = id % CH;
+                sW[buf][row * CH + swz<CH>(row, c)] = __builtin_bit_cast(f16x8, rw[i]);
+            }
+        }
+    };
+
+    f32x4 acc[TN][TM];
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+        for (int b = 0; b < TM; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+
+    const int lrow = lane & 15, lgrp = lane >> 4;
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) gload(kt + 1);
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ++ks) {
+            const int c = ks * 4 + lgrp;
+            f16x8 fw[TN], fa[TM];
+#pragma unroll
+            for (int a = 0; a < TN; ++a) {
+                const int r = wn0 + a * 16 + lrow;
+                fw[a] = sW[cur][r * CH + swz<CH>(r, c)];
+            }
+#pragma unroll
+            for (int b = 0; b < TM; ++b) {
+                const int r = wm0 + b * 16 + lrow;
+                fa[b] = sA[cur][r * CH + swz<CH>(r, c)];
+            }
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+                for (int b = 0; b < TM; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fw[a], fa[b], acc[a][b], 0, 0, 0);
+        }
+        if (kt + 1 < nk) lstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: lane holds D[n][m] for n = nb..nb+3, m = mrow.
+#pragma unroll
+    for (int a = 0; a < TN; ++a) {
+        const int nb = n0 + wn0 + a * 16 + lgrp * 4;
+        float sc[4] = {1.f, 1.f, 1.f, 1.f}, bs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (nb + i < N) {
+                if constexpr (QW) sc[i] = Ws[nb + i];
+                if (bias) bs[i] = h2f(bias[nb + i]);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+            const int m = m0 + wm0 + b * 16 + lrow;
+            if (m >= M) continue;
+            uint16_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float v = acc[a][b][i];
+                if constexpr (QW) v = v * sc[i];
+                o[i] = f2h(v + bs[i]);
+            }
+            uint16_t *dst = C + (size_t)m * N + nb;
+            if (vec_store && nb + 3 < N) {
+                const uint2 pk = {(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+                *reinterpret_cast<uint2 *>(dst) = pk;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (nb + i < N) dst[i] = o[i];
+            }
+        }
+    }
+}
+
+// Any shape, any alignment: 16x16 outputs per work-group, k staged through LDS as fp32.
+template <bool QW>
+__global__ __launch_bounds__(256) void k_gemm_generic(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
+                                                      const void *__restrict__ Wv, const float *__restrict__ Ws,
+                                                      const uint16_t *__restrict__ bias, int M, int N, int K) {
+    __shared__ float sa[16][17], sw[16][17];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int m = blockIdx.y * 16 + ty, n = blockIdx.x * 16 + tx, nw = blockIdx.x * 16 + ty;
+    float acc = 0.f;
+    for (int k0 = 0; k0 < K; k0 += 16) {
+        const int k = k0 + tx;
+        sa[ty][tx] = (m < M && k < K) ? h2f(A[(size_t)m * K + k]) : 0.f;
+        float wv = 0.f;
+        if (nw < N && k < K) {
+            if constexpr (QW) wv = (float)reinterpret_cast<const int8_t *>(Wv)[(size_t)nw * K + k];
+            else wv = h2f(reinterpret_cast<const uint16_t *>(Wv)[(size_t)nw * K + k]);
+        }
+        sw[ty][tx] = wv;
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) acc += sa[ty][kk] * sw[tx][kk];
+        __syncthreads();
+    }
+    if (m < M && n < N) {
+        float v = acc;
+        if constexpr (QW) v *= Ws[n];
+        if (bias) v += h2f(bias[n]);
+        C[(size_t)m * N + n] = f2h(v);
+    }
+}
+
+// One thread per output, bias first, k ascending (the reference's baseline, kernels_naive.cu:44-53).
+__global__ void k_gemm_naive(uint16_t *__restrict__ C, const uint16_t *__restrict__ A, const uint16_t *__restrict__ W,
+                             const uint16_t *__restrict__ bias, int M, int N, int K) {
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)M * N) return;
+    const int m = (int)(idx / N), n = (int)(idx - (long)m * N);
+    float acc = bias ? h2f(bias[n]) : 0.f;
+    for (int k = 0; k < K; ++k) acc += h2f(A[(size_t)m * K + k]) * h2f(W[(size_t)n * K + k]);
+    C[idx] = f2h(acc);
+}
+
+// ---------------------------------------------------------------------------- tile table
+struct GemmCfg {
+    int bn, bm;
+    void (*fp16)(uint16_t *, const uint16_t *, const void *, const float *, const uint16_t *, int, int, int, int, int, int);
+    void (*int8)(uint16_t *, const uint16_t *, const void *, const float *, const uint16_t *, int, int, int, int, int, int);
+    const char *name;
+};
+
+#define G2_CFG(BN, BM, BK, WN, WM) \
+    {BN, BM, k_gemm_mfma<BN, BM, BK, WN, WM, false>, k_gemm_mfma<BN, BM, BK, WN, WM, true>, \
+     "bn" #BN "_bm" #BM "_bk" #BK "_w" #WN "x" #WM}
+
+static const GemmCfg kCfgs[] = {
+    G2_CFG(128, 128, 64, 2, 2),  // 0: wave tile 64x64
+    G2_CFG(128, 64, 64, 2, 2),   // 1: wave tile 64x32
+    G2_CFG(64, 128, 64, 2, 2),   // 2: wave tile 32x64
+    G2_CFG(64, 64, 64, 2, 2),    // 3: wave tile 32x32
+    G2_CFG(128, 32, 64, 4, 1),   // 4: wave tile 32x32
+    G2_CFG(64, 32, 64, 2, 2),    // 5: wave tile 32x16
+    G2_CFG(32, 64, 64, 1, 4),    // 6: wave tile 32x16
+};
+static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
+
+static int g_force_cfg = -2;  // -2: not read yet; -1: table
+
+static int pick_cfg(int M, int N, int K) {
+    if (g_force_cfg == -2) {
+        const char *e = getenv("GPT2_GEMM_CFG");
+        g_force_cfg = e ? atoi(e) : -1;
+        if (g_force_cfg >= kNumCfgs) g_force_cfg = -1;
+    }
+    if (g_force_cfg >= 0) return g_force_cfg;
+    // Pick the largest tile that still gives about one work-group per CU (256 CUs).
+    const long cu = 256;
+    const int order[] = {0, 1, 2, 3, 4, 5};
+    for (int c : order) {
+        const long t = (long)cdiv(N, kCfgs[c].bn) * cdiv(M, kCfgs[c].bm);
+        if (t >= cu) return c;
+    }
+    (void)K;
+    return 5;
+}
+
+static bool mfma_ok(const void *A, const void *W, int K, bool qw) {
+    if (qw) return (K % 16) == 0 && aligned16(A) && aligned16(W);
+    return (K % 8) == 0 && aligned16(A) && aligned16(W);
+}
+
+static void launch_gemm(int cfg, uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const uint16_t *bias,
+                        int M, int N, int K, bool qw) {
+    const GemmCfg &g = kCfgs[cfg];
+    const int tiles_m = cdiv(M, g.bm), tiles_n = cdiv(N, g.bn);
+    const int ntiles = tiles_m * tiles_n;
+    const int vec = (N % 4 == 0) && (((uintptr_t)C & 7u) == 0);
+    auto fn = qw ? g.int8 : g.fp16;
+    hipLaunchKernelGGL(fn, dim3(ntiles), dim3(256), 0, stream(), C, A, W, Ws, bias, M, N, K, tiles_m, ntiles, vec);
+}
+
+static bool gemm_args(const char *who, const void *C, const void *A, const void *W, int M, int N, int K) {
+    if (M < 0 || N < 0 || K < 0) return arg_fail(who);
+    if ((long)M * N > 0 && (!C || !A || !W)) return arg_fail(who);
+    return false;
+}
+
+void gemm(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const uint16_t *bias, int M, int N, int K,
+          bool qw, int cfg) {
+    if ((long)M * N == 0) return;
+    // K == 0 (an empty sum, C = bias or 0) falls through to the generic kernel.
+    if (K > 0 && mfma_ok(A, W, K, qw)) {
+        launch_gemm(cfg >= 0 && cfg < kNumCfgs ? cfg : pick_cfg(M, N, K), C, A, W, Ws, bias, M, N, K, qw);
+        check_launch(qw ? "k_gemm_mfma<int8>" : "k_gemm_mfma<fp16>");
+        return;
+    }
+    dim3 grid(cdiv(N, 16), cdiv(M, 16));
+    if (qw) hipLaunchKernelGGL(k_gemm_generic<true>, grid, dim3(256), 0, stream(), C, A, W, Ws, bias, M, N, K);
+    else hipLaunchKernelGGL(k_gemm_generic<false>, grid, dim3(256), 0, stream(), C, A, W, Ws, bias, M, N, K);
+    check_launch("k_gemm_generic");
+}
+
+}  // namespace g2
+
+using namespace g2;
+
+extern "C" void gpt2_matmul_tiled(gpt2_half *C, const gpt2_half *A, const gpt2_half *W, const gpt2_half *bias,
+                                  int M, int N, int K) {
+    if (gemm_args("gpt2_matmul_tiled: bad shape or null pointer", C, A, W, M, N, K)) return;
+    gemm(C, A, W, nullptr, bias, M, N, K, false, -1);
+}
+
+extern "C" void gpt2_matmul_int8(gpt2_half *C, const gpt2_half *A, const int8_t *Wq, const float *Ws,
+                                 const gpt2_half *bias, int M, int N, int K) {
+    if (gemm_args("gpt2_matmul_int8: bad shape or null pointer", C, A, Wq, M, N, K)) return;
+    if ((long)M * N > 0 && !Ws) { arg_fail("gpt2_matmul_int8: null scales"); return; }
+    gemm(C, A, Wq, Ws, bias, M, N, K, true, -1);
+}
+
+extern "C" void gpt2_matmul_naive(gpt2_half *C, const gpt2_half *A, const gpt2_half *W, const gpt2_half *bias,
+                                  int M, int N, int K) {
+    if (gemm_args("gpt2_matmul_naive: bad shape or null pointer", C, A, W, M, N, K)) return;
+    const long total = (long)M * N;
+    if (total == 0) return;
+    hipLaunchKernelGGL(k_gemm_naive, dim3(cdiv(total, 256)), dim3(256), 0, stream(), C, A, W, bias, M, N, K);
+    check_launch("k_gemm_naive");
+}
+
+// Tuning hooks (not part of the reference interface): run one GEMM with a fixed tile config.
+extern "C" int gpt2_tune_gemm_count(void) { return kNumCfgs; }
+extern "C" const char *gpt2_tune_gemm_name(int cfg) { return cfg >= 0 && cfg < kNumCfgs ? kCfgs[cfg].name : "?"; }
+extern "C" int gpt2_tune_gemm_pick(int M, int N, int K) { return pick_cfg(M, N, K); }
+extern "C" void gpt2_tune_gemm_run(int cfg, gpt2_half *C, const gpt2_half *A, const void *W, const float *Ws,
+                                   const gpt2_half *bias, int M, int N, int K) {
+    if (gemm_args("gpt2_tune_gemm_run", C, A, W, M, N, K)) return;
+    gemm(C, A, W, Ws, bias, M, N, K, Ws != nullptr, cfg);
+}

@@ -1,0 +1,452 @@
+// ops.hip -- the non-matmul kernels a running GPT-2 needs around the matmul path, plus the device
+// quantizer.  Plain and correct; the matmul kernels are where the tuning goes.
+//
+// Numerics follow the reference's GPU kernels: fp16 storage, fp32 arithmetic inside every op,
+//   embed  x = fp16(wte[id] + wpe[t])                          (cuda/kernels_naive.cu:17-23)
+//   LN     mean, then biased variance of (x - mean), eps 1e-5 inside the sqrt
+//                                                              (cuda/kernels_naive.cu:26-41)
+//   gelu   0.5 v (1 + tanh(0.7978845608 (v + 0.044715 v^3)))  (cuda/kernels_naive.cu:85-91)
+//   attention: causal, scale 1/sqrt(64), online softmax       (cuda/kernels_fused.cu:58-140)
+//   decode attention over the [H][maxT][D] cache               (cuda/kvcache.cu:88-129)
+// The INT8 quantizer restates tools/quantize.py:58-73 on the GPU (see k_quantize_rows).
+#include <cmath>
+
+#include "common.h"
+
+namespace g2 {
+
+// ------------------------------------------------------------------ embed
+__global__ void k_embed(uint16_t *__restrict__ x, const uint16_t *__restrict__ wte, const uint16_t *__restrict__ wpe,
+                        const int *__restrict__ ids, int T, int E) {
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)T * E) return;
+    const int t = (int)(idx / E), e = (int)(idx - (long)t * E);
+    const int id = ids[t];
+    // Out-of-vocabulary ids read nothing (an unchecked gather would fault) and embed as wpe alone.
+    const float te = ((unsigned)id < (unsigned)GPT2_VOCAB) ? h2f(wte[(size_t)id * E + e]) : 0.f;
+    x[idx] = f2h(te + h2f(wpe[(size_t)t * E + e]));
+}
+
+__global__ void k_embed_one(uint16_t *__restrict__ x, const uint16_t *__restrict__ wte,
+                            const uint16_t *__restrict__ wpe, StepArg st, int E) {
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const int id = st.tok(), pos = st.p();
+    const float te = ((unsigned)id < (unsigned)GPT2_VOCAB) ? h2f(wte[(size_t)id * E + e]) : 0.f;
+    const float pe = ((unsigned)pos < (unsigned)GPT2_N_CTX) ? h2f(wpe[(size_t)pos * E + e]) : 0.f;
+    x[e] = f2h(te + pe);
+}
+
+// ------------------------------------------------------------------ LayerNorm: one wave per row
+template <bool VEC768>
+__global__ __launch_bounds__(256) void k_layernorm(uint16_t *__restrict__ out, const uint16_t *__restrict__ x,
+                                                   const uint16_t *__restrict__ g, const uint16_t *__restrict__ b,
+                                                   int M, int E) {
+    const int lane = threadIdx.x & 63;
+    const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (row >= M) return;
+    const uint16_t *xr = x + (size_t)row * E;
+    uint16_t *o = out + (size_t)row * E;
+    if constexpr (VEC768) {
+        // 768 = 3 x (64 lanes x 4 halves): keep the row in registers between the passes
+        float v[12];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const f16x4 h = *reinterpret_cast<const f16x4 *>(xr + 256 * i + 4 * lane);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[4 * i + c] = (float)h[c];
+        }
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 12; ++i) s += v[i];
+        const float mean = wave_sum(s) / E;
+        float q = 0.f;
+#pragma unroll
+        for (int i = 0; i < 12; ++i) {
+            const float d = v[i] - mean;
+            q += d * d;
+        }
+        const float rstd = 1.0f / sqrtf(wave_sum(q) / E + GPT2_LN_EPS);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int e0 = 256 * i + 4 * lane;
+            const f16x4 gg = *reinterpret_cast<const f16x4 *>(g + e0);
+            const f16x4 bb = *reinterpret_cast<const f16x4 *>(b + e0);
+            f16x4 r;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) r[c] = (f16)((v[4 * i + c] - mean) * rstd * (float)gg[c] + (float)bb[c]);
+            *reinterpret_cast<f16x4 *>(o + e0) = r;
+        }
+        return;
+    } else {
+    float s = 0.f;
+    for (int e = lane; e < E; e += 64) s += h2f(xr[e]);
+    const float mean = wave_sum(s) / E;
+    float q = 0.f;
+    for (int e = lane; e < E; e += 64) {
+        const float d = h2f(xr[e]) - mean;
+        q += d * d;
+    }
+    const float rstd = 1.0f / sqrtf(wave_sum(q) / E + GPT2_LN_EPS);
+    for (int e = lane; e < E; e += 64) o[e] = f2h((h2f(xr[e]) - mean) * rstd * h2f(g[e]) + h2f(b[e]));
+    }
+}
+
+// ------------------------------------------------------------------ gelu / add
+__device__ __forceinline__ float gelu_new(float v) {
+    const float z = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+    return 0.5f * v * (1.0f + tanhf(z));
+}
+
+__global__ void k_gelu(uint16_t *__restrict__ x, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    x[i] = f2h(gelu_new(h2f(x[i])));
+}
+
+__global__ void k_gelu8(f16x8 *__restrict__ x, size_t n8) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n8) return;
+    f16x8 v = x[i];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) v[c] = (f16)gelu_new((float)v[c]);
+    x[i] = v;
+}
+
+__global__ void k_add(uint16_t *__restrict__ x, const uint16_t *__restrict__ y, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    x[i] = f2h(h2f(x[i]) + h2f(y[i]));
+}
+
+__global__ void k_add8(f16x8 *__restrict__ x, const f16x8 *__restrict__ y, size_t n8) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n8) return;
+    f16x8 a = x[i];
+    const f16x8 b = y[i];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) a[c] = (f16)((float)a[c] + (float)b[c]);
+    x[i] = a;
+}
+
+// ------------------------------------------------------------------ attention
+// One wave attends one query (64 dims) over keys [j0, j1) of one head.  Keys are rows
+// `kbase + j*stride`, values `vbase + j*stride` (halves).  Lane = key inside a 64-key chunk for the
+// scores; for the context, lanes 0-31 take even keys and lanes 32-63 odd keys, two dims per lane.
+// Running state: max m, exp-sum l, context (c0, c1) for dims 2*(lane&31) and +1.
+struct AttnState {
+    float m, l, c0, c1;
+};
+
+__device__ __forceinline__ void attend_range(const f16x8 (&q)[8], const uint16_t *__restrict__ kbase,
+                                             const uint16_t *__restrict__ vbase, long stride, int j0, int j1,
+                                             float scale, AttnState &st) {
+    const int lane = threadIdx.x & 63;
+    const int half = lane >> 5, d2 = 2 * (lane & 31);
+    for (int jc = j0; jc < j1; jc += 64) {
+        const int j = jc + lane;
+        float s = -INFINITY;
+        if (j < j1) {
+            const uint16_t *kr = kbase + (size_t)j * stride;
+            float dot = 0.f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const f16x8 kk = *reinterpret_cast<const f16x8 *>(kr + 8 * c);
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    dot = __builtin_amdgcn_fdot2(f16x2{q[c][2 * t], q[c][2 * t + 1]}, f16x2{kk[2 * t], kk[2 * t + 1]},
+                                                 dot, false);
+            }
+            s = dot * scale;
+        }
+        const float mnew = fmaxf(st.m, wave_max(s));   // finite: key jc < j1 is in range
+        const float p = (j < j1) ? __expf(s - mnew) : 0.f;
+        const float corr = __expf(st.m - mnew);         // st.m = -inf on the first chunk -> 0
+        st.l = st.l * corr + wave_sum(p);
+        st.c0 *= corr;
+        st.c1 *= corr;
+        st.m = mnew;
+        const int nkeys = min(64, j1 - jc);
+        for (int jj = 0; jj < nkeys; jj += 2) {
+            const int key = jj + half;
+            const float pj = __shfl(p, key, 64);
+            if (key < nkeys) {
+                const f16x2 vv = *reinterpret_cast<const f16x2 *>(vbase + (size_t)(jc + key) * stride + d2);
+                st.c0 += pj * (float)vv[0];
+                st.c1 += pj * (float)vv[1];
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void load_q(f16x8 (&q)[8], const uint16_t *qp) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) q[c] = *reinterpret_cast<const f16x8 *>(qp + 8 * c);
+}
+
+// Prefill: grid (ceil(T/4), H), four waves = four consecutive queries of one head.
+__global__ __launch_bounds__(256) void k_attention_prefill(uint16_t *__restrict__ att, const uint16_t *__restrict__ qkv,
+                                                           int T) {
+    constexpr int E = GPT2_N_EMBD, D = GPT2_HEAD_DIM, S = 3 * GPT2_N_EMBD;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int h = blockIdx.y, i = blockIdx.x * 4 + w;
+    if (i >= T) return;
+    f16x8 q[8];
+    load_q(q, qkv + (size_t)i * S + h * D);
+    AttnState st = {-INFINITY, 0.f, 0.f, 0.f};
+    attend_range(q, qkv + E + h * D, qkv + 2 * E + h * D, S, 0, i + 1, 0.125f, st);
+    st.c0 += __shfl_xor(st.c0, 32, 64);
+    st.c1 += __shfl_xor(st.c1, 32, 64);
+    if (lane < 32) {
+        const float inv = 1.0f / st.l;
+        f16x2 r = {(f16)(st.c0 * inv), (f16)(st.c1 * inv)};
+        *reinterpret_cast<f16x2 *>(att + (size_t)i * E + h * D + 2 * lane) = r;
+    }
+}
+
+// Decode: one work-group per head, NW waves split the keys [0, len); partial (m, l, c) states are
+// merged through LDS.  len = pos + 1 comes from the step argument.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void k_attn_decode(uint16_t *__restrict__ att, const uint16_t *__restrict__ qkv,
+                                                         const uint16_t *__restrict__ Kc, const uint16_t *__restrict__ Vc,
+                                                         int maxT, StepArg st_arg, int len_imm) {
+    constexpr int D = GPT2_HEAD_DIM;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, h = blockIdx.x;
+    const int len = min(len_imm > 0 ? len_imm : st_arg.p() + 1, maxT);
+    const int per = ((len + NW - 1) / NW + 63) & ~63;
+    const int j0 = min(len, w * per), j1 = min(len, j0 + per);
+    f16x8 q[8];
+    load_q(q, qkv + h * D);
+    AttnState st = {-INFINITY, 0.f, 0.f, 0.f};
+    const uint16_t *kb = Kc + (size_t)h * maxT * D, *vb = Vc + (size_t)h * maxT * D;
+    if (j0 < j1) attend_range(q, kb, vb, D, j0, j1, 0.125f, st);
+    st.c0 += __shfl_xor(st.c0, 32, 64);
+    st.c1 += __shfl_xor(st.c1, 32, 64);
+    __shared__ float sm[NW], sl[NW], sc[NW][D];
+    if (lane == 0) {
+        sm[w] = st.m;
+        sl[w] = st.l;
+    }
+    if (lane < 32) {
+        sc[w][2 * lane] = st.c0;
+        sc[w][2 * lane + 1] = st.c1;
+    }
+    __syncthreads();
+    if (w == 0) {
+        float mx = -INFINITY;
+        for (int i = 0; i < NW; ++i) mx = fmaxf(mx, sm[i]);
+        float L = 0.f, c = 0.f;
+        for (int i = 0; i < NW; ++i) {
+            if (sl[i] == 0.f) continue;   // wave had no keys
+            const float f = __expf(sm[i] - mx);
+            L += sl[i] * f;
+            c += sc[i][lane] * f;
+        }
+        att[h * D + lane] = f2h(c / L);
+    }
+}
+
+// ------------------------------------------------------------------ KV cache writes
+// Layout per layer: K[h][pos][d], V[h][pos][d] with d fastest (cuda/kvcache.cuh:150-151).
+__global__ void k_kv_scatter(uint16_t *__restrict__ K, uint16_t *__restrict__ V, const uint16_t *__restrict__ qkv,
+                             int T, int maxT) {
+    constexpr int E = GPT2_N_EMBD, D = GPT2_HEAD_DIM;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;   // one 8-half chunk each
+    if (idx >= (long)T * (E / 8)) return;
+    const int t = (int)(idx / (E / 8)), c = (int)(idx % (E / 8));
+    const int e = c * 8, h = e / D, d = e % D;
+    const size_t off = ((size_t)h * maxT + t) * D + d;
+    const uint16_t *row = qkv + (size_t)t * 3 * E;
+    *reinterpret_cast<f16x8 *>(K + off) = *reinterpret_cast<const f16x8 *>(row + E + e);
+    *reinterpret_cast<f16x8 *>(V + off) = *reinterpret_cast<const f16x8 *>(row + 2 * E + e);
+}
+
+__global__ void k_kv_append(uint16_t *__restrict__ K, uint16_t *__restrict__ V, const uint16_t *__restrict__ qkv,
+                            StepArg st, int maxT) {
+    constexpr int E = GPT2_N_EMBD, D = GPT2_HEAD_DIM;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= E) return;
+    const int pos = st.p();
+    if ((unsigned)pos >= (unsigned)maxT) return;
+    const int h = i / D, d = i % D;
+    const size_t off = ((size_t)h * maxT + pos) * D + d;
+    K[off] = qkv[E + i];
+    V[off] = qkv[2 * E + i];
+}
+
+// ------------------------------------------------------------------ greedy next token
+// Argmax over fp16 logits[V] (lowest index among equal maxima, like argmax in
+// bench/kv_gate.cu:56); writes tokens[pos+1] and advances the device state {token, pos}.
+__global__ __launch_bounds__(1024) void k_argmax_advance(const uint16_t *__restrict__ logits, int V, int *__restrict__ state,
+                                                         int *__restrict__ tokens, int max_pos) {
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = threadIdx.x; i < V; i += blockDim.x) {
+        const float v = h2f(logits[i]);
+        if (v > best) { best = v; bi = i; }   // i increases, so ties keep the first
+    }
+    for (int o = 1; o < 64; o <<= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+    }
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { sv[w] = best; si[w] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int nw = blockDim.x >> 6;
+        for (int i = 1; i < nw; ++i)
+            if (sv[i] > best || (sv[i] == best && si[i] < bi)) { best = sv[i]; bi = si[i]; }
+        if (bi == 0x7fffffff) bi = 0;   // all NaN: token 0
+        const int next = state[1] + 1;
+        if (tokens && next < max_pos) tokens[next] = bi;
+        state[0] = bi;
+        state[1] = next;
+    }
+}
+
+// ------------------------------------------------------------------ INT8 quantizer
+// One wave per output row of an fp16 [N,K] tensor (tools/quantize.py:58-73):
+//   absmax = max_k |w|;  s = absmax == 0 ? 1 : fl32(absmax / 127);  q = clamp(rint(fl32(w / s)), +-127)
+// The divisions are IEEE float divisions (this file is built without fast-math; HIP's default
+// float division is correctly rounded) and rintf is v_rndne_f32 (half to even).
+__global__ __launch_bounds__(256) void k_quantize_rows(int8_t *__restrict__ q, float *__restrict__ s,
+                                                       const uint16_t *__restrict__ w, int N, int K) {
+    const int lane = threadIdx.x & 63;
+    const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (row >= N) return;
+    const uint16_t *wr = w + (size_t)row * K;
+    float peak = 0.f;
+    for (int k = lane; k < K; k += 64) peak = fmaxf(peak, fabsf(h2f(wr[k])));
+    peak = wave_max(peak);
+    const float scale = (peak == 0.f) ? 1.0f : peak / 127.0f;
+    if (lane == 0) s[row] = scale;
+    int8_t *qr = q + (size_t)row * K;
+    for (int k = lane; k < K; k += 64) {
+        float r = rintf(h2f(wr[k]) / scale);
+        r = fminf(fmaxf(r, -127.0f), 127.0f);
+        qr[k] = (int8_t)(int)r;
+    }
+}
+
+// ------------------------------------------------------------------ host launchers (internal)
+void embed_one(uint16_t *x, const uint16_t *wte, const uint16_t *wpe, StepArg st) {
+    hipLaunchKernelGGL(k_embed_one, dim3(cdiv(GPT2_N_EMBD, 256)), dim3(256), 0, stream(), x, wte, wpe, st, GPT2_N_EMBD);
+    check_launch("k_embed_one");
+}
+
+void kv_append(uint16_t *K, uint16_t *V, const uint16_t *qkv, StepArg st, int maxT) {
+    hipLaunchKernelGGL(k_kv_append, dim3(cdiv(GPT2_N_EMBD, 256)), dim3(256), 0, stream(), K, V, qkv, st, maxT);
+    check_launch("k_kv_append");
+}
+
+void attn_decode(uint16_t *att, const uint16_t *qkv, const uint16_t *K, const uint16_t *V, int maxT, StepArg st,
+                 int len_imm) {
+    hipLaunchKernelGGL(k_attn_decode<8>, dim3(GPT2_N_HEAD), dim3(512), 0, stream(), att, qkv, K, V, maxT, st, len_imm);
+    check_launch("k_attn_decode");
+}
+
+void argmax_advance(const uint16_t *logits, int V, int *state, int *tokens, int max_pos) {
+    hipLaunchKernelGGL(k_argmax_advance, dim3(1), dim3(1024), 0, stream(), logits, V, state, tokens, max_pos);
+    check_launch("k_argmax_advance");
+}
+
+}  // namespace g2
+
+using namespace g2;
+
+extern "C" void gpt2_embed(gpt2_half *x, const gpt2_half *wte, const gpt2_half *wpe, const int *ids, int T, int E) {
+    if (T <= 0 || E <= 0) return;
+    if (!x || !wte || !wpe || !ids) { arg_fail("gpt2_embed: null pointer"); return; }
+    const long n = (long)T * E;
+    hipLaunchKernelGGL(k_embed, dim3(cdiv(n, 256)), dim3(256), 0, stream(), x, wte, wpe, ids, T, E);
+    check_launch("k_embed");
+}
+
+extern "C" void gpt2_layernorm(gpt2_half *out, const gpt2_half *x, const gpt2_half *g, const gpt2_half *b, int M,
+                               int E) {
+    if (M <= 0 || E <= 0) return;
+    if (!out || !x || !g || !b) { arg_fail("gpt2_layernorm: null pointer"); return; }
+    if (E == GPT2_N_EMBD && !(((uintptr_t)x | (uintptr_t)out | (uintptr_t)g | (uintptr_t)b) & 7u))
+        hipLaunchKernelGGL(k_layernorm<true>, dim3(cdiv(M, 4)), dim3(256), 0, stream(), out, x, g, b, M, E);
+    else
+        hipLaunchKernelGGL(k_layernorm<false>, dim3(cdiv(M, 4)), dim3(256), 0, stream(), out, x, g, b, M, E);
+    check_launch("k_layernorm");
+}
+
+extern "C" void gpt2_gelu(gpt2_half *x, size_t n) {
+    if (n == 0) return;
+    if (!x) { arg_fail("gpt2_gelu: null pointer"); return; }
+    if (n % 8 == 0 && aligned16(x)) {
+        hipLaunchKernelGGL(k_gelu8, dim3(cdiv((long)(n / 8), 256)), dim3(256), 0, stream(), (f16x8 *)x, n / 8);
+    } else {
+        hipLaunchKernelGGL(k_gelu, dim3(cdiv((long)n, 256)), dim3(256), 0, stream(), x, n);
+    }
+    check_launch("k_gelu");
+}
+
+extern "C" void gpt2_add(gpt2_half *x, const gpt2_half *y, size_t n) {
+    if (n == 0) return;
+    if (!x || !y) { arg_fail("gpt2_add: null pointer"); return; }
+    if (n % 8 == 0 && aligned16(x) && aligned16(y)) {
+        hipLaunchKernelGGL(k_add8, dim3(cdiv((long)(n / 8), 256)), dim3(256), 0, stream(), (f16x8 *)x,
+                           (const f16x8 *)y, n / 8);
+    } else {
+        hipLaunchKernelGGL(k_add, dim3(cdiv((long)n, 256)), dim3(256), 0, stream(), x, y, n);
+    }
+    check_launch("k_add");
+}
+
+extern "C" void gpt2_attention_flash(gpt2_half *att, const gpt2_half *qkv, int T, int E, int H, int D) {
+    if (T <= 0) return;
+    if (E != GPT2_N_EMBD || H != GPT2_N_HEAD || D != GPT2_HEAD_DIM || T > GPT2_N_CTX) {
+        arg_fail("gpt2_attention_flash: only E=768, H=12, D=64, T<=1024");
+        return;
+    }
+    if (!att || !qkv || !aligned16(att) || !aligned16(qkv)) { arg_fail("gpt2_attention_flash: null/unaligned"); return; }
+    hipLaunchKernelGGL(k_attention_prefill, dim3(cdiv(T, 4), GPT2_N_HEAD), dim3(256), 0, stream(), att, qkv, T);
+    check_launch("k_attention_prefill");
+}
+
+extern "C" void gpt2_quantize_rows(int8_t *q, float *s, const gpt2_half *w, int N, int K) {
+    if (N <= 0 || K <= 0) return;
+    if (!q || !s || !w) { arg_fail("gpt2_quantize_rows: null pointer"); return; }
+    hipLaunchKernelGGL(k_quantize_rows, dim3(cdiv(N, 4)), dim3(256), 0, stream(), q, s, w, N, K);
+    check_launch("k_quantize_rows");
+}
+
+extern "C" void gpt2_kv_scatter_prefill(GPT2KVCache *kv, int L, const gpt2_half *qkv, int T) {
+    if (T <= 0) return;
+    if (!kv || !kv->data || !qkv || L < 0 || L >= kv->nLayer || T > kv->maxT || !aligned16(qkv)) {
+        arg_fail("gpt2_kv_scatter_prefill: bad cache, layer or length");
+        return;
+    }
+    const long n = (long)T * (GPT2_N_EMBD / 8);
+    hipLaunchKernelGGL(k_kv_scatter, dim3(cdiv(n, 256)), dim3(256), 0, stream(), gpt2_kv_K(kv, L), gpt2_kv_V(kv, L),
+                       qkv, T, kv->maxT);
+    check_launch("k_kv_scatter");
+}
+
+extern "C" void gpt2_embed_one(gpt2_half *x, const gpt2_half *wte, const gpt2_half *wpe, int token, int pos) {
+    if (!x || !wte || !wpe) { arg_fail("gpt2_embed_one: null pointer"); return; }
+    if (token < 0 || token >= GPT2_VOCAB || pos < 0 || pos >= GPT2_N_CTX) { arg_fail("gpt2_embed_one: token/pos range"); return; }
+    embed_one(x, wte, wpe, StepArg{token, pos, nullptr});
+}
+
+extern "C" void gpt2_kv_append_one(GPT2KVCache *kv, int L, const gpt2_half *qkv, int pos) {
+    if (!kv || !kv->data || !qkv || L < 0 || L >= kv->nLayer || pos < 0 || pos >= kv->maxT) {
+        arg_fail("gpt2_kv_append_one: bad cache, layer or position");
+        return;
+    }
+    kv_append(gpt2_kv_K(kv, L), gpt2_kv_V(kv, L), qkv, StepArg{0, pos, nullptr}, kv->maxT);
+}
+
+extern "C" void gpt2_attn_decode(gpt2_half *att, const gpt2_half *qkv, const GPT2KVCache *kv, int L, int len) {
+    if (!kv || !kv->data || !att || !qkv || L < 0 || L >= kv->nLayer || len <= 0 || len > kv->maxT || !aligned16(qkv)) {
+        arg_fail("gpt2_attn_decode: bad cache, layer or length");
+        return;
+    }
+    attn_decode(att, qkv, gpt2_kv_K(kv, L), gpt2_kv_V(kv, L), kv->maxT, StepArg{0, 0, nullptr}, len);
+}
