@@ -157,13 +157,20 @@ SIGNATURES = {
     "gpt2_decode_graph_run": (_i, [_vp, _i]),
     "gpt2_decode_graph_sync": (_i, [_vp, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "gpt2_decode_graph_destroy": (None, [_vp]),
+    "gpt2_decode_graph_time": (_i, [_vp, _i, _fp]),
     # bench / tuning hooks (not part of the reference interface)
     "gpt2_bench_ops": (_i, [C.POINTER(GPT2BenchOp), _i, _i, _i, _fp, _fp]),
     "gpt2_bench_time": (_i, [_vp, _vp, _fp]),
     "gpt2_device_info": (_i, [C.POINTER(_i), C.POINTER(_i), C.c_char_p, _i]),
+    "gpt2_bench_empty": (_i, [_i, _fp]),
+    "gpt2_bench_read": (_i, [_vp, _sz, _i, _fp]),
+    "gpt2_bench_mfma": (_i, [_i, _i, _fp]),
+    "gpt2_bench_copy": (_i, [_vp, _vp, _sz, _fp]),
     "gpt2_tune_gemm_count": (_i, []),
     "gpt2_tune_gemm_name": (C.c_char_p, [_i]),
     "gpt2_tune_gemm_pick": (_i, [_i, _i, _i]),
+    "gpt2_tune_gemm_fits": (_i, [_i, _i]),
+    "gpt2_tune_gemm_force": (None, [_i]),
     "gpt2_tune_gemm_run": (None, [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
     "gpt2_tune_gemv_count": (_i, []),
     "gpt2_tune_gemv_name": (C.c_char_p, [_i]),

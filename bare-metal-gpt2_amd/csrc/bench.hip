@@ -100,3 +100,137 @@ int gpt2_device_info(int *cus, int *clock_khz, char *name, int name_len) {
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------------------------------------------
+// Roofline denominators (the role of bench/microbench.cu:51-208 in the reference): the dispatch
+// floor of an empty kernel, an HBM read stream, and the fp16 MFMA issue rate.
+
+__global__ void k_empty() {}
+
+// Each thread streams 16-byte vectors with a grid stride and folds them into one word so the loads
+// cannot be removed; one word per block is written.
+__global__ __launch_bounds__(256) void k_read_stream(const i32x4 *__restrict__ src, size_t n16, int *__restrict__ sink) {
+    i32x4 acc = {0, 0, 0, 0};
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const i32x4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+        acc ^= a ^ b ^ c ^ d;
+    }
+    for (; i < n16; i += stride) acc ^= src[i];
+    const int v = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    if (v == 0x7fffffff) sink[blockIdx.x] = v;   // practically never taken; keeps the loads live
+}
+
+// Eight independent accumulators per wave, `iters` rounds of v_mfma_f32_16x16x32_f16 each.
+__global__ __launch_bounds__(256) void k_mfma_peak(float *__restrict__ out, int iters) {
+    f16x8 a, b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        a[i] = (f16)(0.001f * (threadIdx.x + i));
+        b[i] = (f16)(0.002f * (threadIdx.x - i));
+    }
+    f32x4 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[j], 0, 0, 0);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += acc[j][0];
+    if (s == 12345.678f) out[blockIdx.x] = s;
+}
+
+extern "C" {
+
+// Mean milliseconds per launch of an empty kernel (grid 1 x 64), back to back.
+int gpt2_bench_empty(int iters, float *ms) {
+    hipStream_t s = (hipStream_t)gpt2_get_stream();
+    hipEvent_t a, b;
+    hipEventCreate(&a);
+    hipEventCreate(&b);
+    for (int i = 0; i < 10; ++i) hipLaunchKernelGGL(k_empty, dim3(1), dim3(64), 0, s);
+    hipStreamSynchronize(s);
+    hipEventRecord(a, s);
+    for (int i = 0; i < iters; ++i) hipLaunchKernelGGL(k_empty, dim3(1), dim3(64), 0, s);
+    hipEventRecord(b, s);
+    hipEventSynchronize(b);
+    hipEventElapsedTime(ms, a, b);
+    *ms /= iters;
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    return gpt2_last_error();
+}
+
+// Read-stream GB/s over `bytes` of device memory (use >> 256 MB so the MALL cannot hold it).
+int gpt2_bench_read(const void *buf, size_t bytes, int iters, float *ms) {
+    hipStream_t s = (hipStream_t)gpt2_get_stream();
+    int *sink = (int *)gpt2_dmalloc(4096 * 4);
+    if (!sink) return 1;
+    const size_t n16 = bytes / 16;
+    const int blocks = 256 * 16;
+    hipEvent_t a, b;
+    hipEventCreate(&a);
+    hipEventCreate(&b);
+    hipLaunchKernelGGL(k_read_stream, dim3(blocks), dim3(256), 0, s, (const i32x4 *)buf, n16, sink);
+    hipStreamSynchronize(s);
+    hipEventRecord(a, s);
+    for (int i = 0; i < iters; ++i)
+        hipLaunchKernelGGL(k_read_stream, dim3(blocks), dim3(256), 0, s, (const i32x4 *)buf, n16, sink);
+    hipEventRecord(b, s);
+    hipEventSynchronize(b);
+    hipEventElapsedTime(ms, a, b);
+    *ms /= iters;
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    gpt2_dfree(sink);
+    return gpt2_last_error();
+}
+
+// fp16 MFMA issue rate: returns milliseconds for `iters` rounds on `blocks` work-groups of 4 waves;
+// FLOP = blocks * 4 waves * iters * 8 * 16*16*32*2.
+int gpt2_bench_mfma(int blocks, int iters, float *ms) {
+    hipStream_t s = (hipStream_t)gpt2_get_stream();
+    float *out = (float *)gpt2_dmalloc(blocks * 4);
+    if (!out) return 1;
+    hipEvent_t a, b;
+    hipEventCreate(&a);
+    hipEventCreate(&b);
+    hipLaunchKernelGGL(k_mfma_peak, dim3(blocks), dim3(256), 0, s, out, 16);
+    hipStreamSynchronize(s);
+    hipEventRecord(a, s);
+    hipLaunchKernelGGL(k_mfma_peak, dim3(blocks), dim3(256), 0, s, out, iters);
+    hipEventRecord(b, s);
+    hipEventSynchronize(b);
+    hipEventElapsedTime(ms, a, b);
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    gpt2_dfree(out);
+    return gpt2_last_error();
+}
+
+}  // extern "C"
+
+// Plain 16-byte copy of a known size: the calibration point for the FETCH_SIZE / WRITE_SIZE
+// counters (HBM bytes per dispatch) used to report a kernel's measured traffic.
+__global__ __launch_bounds__(256) void k_copy16(i32x4 *__restrict__ dst, const i32x4 *__restrict__ src, size_t n16) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+}
+
+extern "C" int gpt2_bench_copy(void *dst, const void *src, size_t bytes, float *ms) {
+    hipStream_t s = (hipStream_t)gpt2_get_stream();
+    hipEvent_t a, b;
+    hipEventCreate(&a);
+    hipEventCreate(&b);
+    hipEventRecord(a, s);
+    hipLaunchKernelGGL(k_copy16, dim3(4096), dim3(256), 0, s, (i32x4 *)dst, (const i32x4 *)src, bytes / 16);
+    hipEventRecord(b, s);
+    hipEventSynchronize(b);
+    hipEventElapsedTime(ms, a, b);
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    return gpt2_last_error();
+}

@@ -397,6 +397,24 @@ extern "C" int gpt2_decode_graph_sync(GPT2DecodeGraph *g, int *token, int *pos) 
     return 0;
 }
 
+// Bench hook: mean milliseconds per replay over `steps` back-to-back replays, timed with events on
+// the graph's own stream.
+extern "C" int gpt2_decode_graph_time(GPT2DecodeGraph *g, int steps, float *ms) {
+    if (!g || steps <= 0 || !ms) return 1;
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) return 1;
+    hipEventRecord(a, g->stream);
+    const int rc = gpt2_decode_graph_run(g, steps);
+    hipEventRecord(b, g->stream);
+    hipEventSynchronize(b);
+    float t = 0.f;
+    hipEventElapsedTime(&t, a, b);
+    *ms = t / steps;
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    return rc;
+}
+
 extern "C" void gpt2_decode_graph_destroy(GPT2DecodeGraph *g) {
     if (!g) return;
     hipStreamSynchronize(g->stream);

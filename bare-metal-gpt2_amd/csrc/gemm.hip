@@ -25,10 +25,11 @@
 
 namespace g2 {
 
-// 16-byte chunk swizzle inside an LDS row of CH chunks (CH = 4 or 8).
+// 16-byte chunk swizzle inside an LDS row of CH chunks.  Eight consecutive rows read at one
+// logical chunk land on eight distinct 16-byte bank groups (measured: zero SQ_LDS_BANK_CONFLICT).
 template <int CH>
 __device__ __forceinline__ int swz(int row, int c) {
-    if constexpr (CH == 8) return c ^ (row & 7);
+    if constexpr (CH >= 8) return c ^ (row & 7);
     else return c ^ ((row >> 1) & 3);
 }
 
@@ -50,7 +51,8 @@ __device__ __forceinline__ int xcd_tile(int bid, int ntiles) {
     return xcd * per + (xcd < rem ? xcd : rem) + slot;
 }
 
-template <int BN, int BM, int BK, int WN, int WM, bool QW>
+// GUARD: any K % 8 == 0 (predicated, zero-filled loads); otherwise K % (BK * DEPTH) == 0.
+template <int BN, int BM, int BK, int WN, int WM, bool QW, int DEPTH, bool GUARD = false>
 __global__ __launch_bounds__(256) void k_gemm_mfma(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
                                                    const void *__restrict__ Wv, const float *__restrict__ Ws,
                                                    const uint16_t *__restrict__ bias, int M, int N, int K,
@@ -73,17 +75,26 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(uint16_t *__restrict__ C, con
     const int nk = (K + BK - 1) / BK;
 
     const f16x8 zero8 = {};
-    f16x8 ra[NLA];
-    i32x4 rw[NLW];
+    // Register ring: DEPTH k-tiles of global loads are in flight while one is consumed.
+    f16x8 rra[DEPTH][NLA];
+    i32x4 rrw[DEPTH][NLW];
 
-    auto gload = [&](int kt) {
+    // Without GUARD, loads are never predicated: rows past M or N read the last valid row (their
+    // results are not stored) and K is a multiple of BK*DEPTH, so every tile issues the same number of
+    // loads and the compiler can count them (s_waitcnt vmcnt(n) on the oldest ring slot only).
+    auto gload = [&](int kt, f16x8 (&ra)[NLA], i32x4 (&rw)[NLW]) {
         const int k0 = kt * BK;
 #pragma unroll
         for (int i = 0; i < NLA; ++i) {
             const int id = tid + 256 * i, row = id / CH, c = id % CH;
             if (GA % 256 != 0 && id >= GA) break;
-            const int m = m0 + row, k = k0 + c * 8;
-            ra[i] = (m < M && k < K) ? *reinterpret_cast<const f16x8 *>(A + (size_t)m * K + k) : zero8;
+            if constexpr (GUARD) {
+                const int m = m0 + row, k = k0 + c * 8;
+                ra[i] = (m < M && k < K) ? *reinterpret_cast<const f16x8 *>(A + (size_t)m * K + k) : zero8;
+            } else {
+                const int m = min(m0 + row, M - 1);
+                ra[i] = *reinterpret_cast<const f16x8 *>(A + (size_t)m * K + k0 + c * 8);
+            }
         }
 #pragma unroll
         for (int i = 0; i < NLW; ++i) {
@@ -92,18 +103,28 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(uint16_t *__restrict__ C, con
             if constexpr (QW) {
                 constexpr int CQ = CH / 2;   // 16-byte int8 chunks per row
                 const int row = id / CQ, c = id % CQ;
-                const int n = n0 + row, k = k0 + c * 16;
-                const int8_t *W = reinterpret_cast<const int8_t *>(Wv);
-                rw[i] = (n < N && k < K) ? *reinterpret_cast<const i32x4 *>(W + (size_t)n * K + k) : i32x4{0, 0, 0, 0};
+                const int8_t *src = reinterpret_cast<const int8_t *>(Wv);
+                if constexpr (GUARD) {
+                    const int n = n0 + row, k = k0 + c * 16;
+                    rw[i] = (n < N && k < K) ? *reinterpret_cast<const i32x4 *>(src + (size_t)n * K + k) : i32x4{0, 0, 0, 0};
+                } else {
+                    const int n = min(n0 + row, N - 1);
+                    rw[i] = *reinterpret_cast<const i32x4 *>(src + (size_t)n * K + k0 + c * 16);
+                }
             } else {
                 const int row = id / CH, c = id % CH;
-                const int n = n0 + row, k = k0 + c * 8;
-                const uint16_t *W = reinterpret_cast<const uint16_t *>(Wv);
-                rw[i] = (n < N && k < K) ? *reinterpret_cast<const i32x4 *>(W + (size_t)n * K + k) : i32x4{0, 0, 0, 0};
+                const uint16_t *src = reinterpret_cast<const uint16_t *>(Wv);
+                if constexpr (GUARD) {
+                    const int n = n0 + row, k = k0 + c * 8;
+                    rw[i] = (n < N && k < K) ? *reinterpret_cast<const i32x4 *>(src + (size_t)n * K + k) : i32x4{0, 0, 0, 0};
+                } else {
+                    const int n = min(n0 + row, N - 1);
+                    rw[i] = *reinterpret_cast<const i32x4 *>(src + (size_t)n * K + k0 + c * 8);
+                }
             }
         }
     };
-    auto lstore = [&](int buf) {
+    auto lstore = [&](int buf, const f16x8 (&ra)[NLA], const i32x4 (&rw)[NLW]) {
 #pragma unroll
         for (int i = 0; i < NLA; ++i) {
             const int id = tid + 256 * i, row = id / CH, c = id % CH;
@@ -139,36 +160,57 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(uint16_t *__restrict__ C, con
 #pragma unroll
         for (int b = 0; b < TM; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
-
     const int lrow = lane & 15, lgrp = lane >> 4;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) gload(kt + 1);
+
+    // Software pipeline, one barrier per k-tile.  At the top of iteration kt, LDS buffer kt&1 holds
+    // tile kt and ring slot t % DEPTH holds (or is loading) tile t for t in kt+1 .. kt+DEPTH.  The
+    // iteration reads tile kt's fragments, then stores tile kt+1 into the other LDS buffer and
+    // refills its ring slot with tile kt+1+DEPTH, then runs the MFMAs: LDS writes, global loads and
+    // MFMAs of one wave are in flight together.  The buffer written at kt was last read at kt-1,
+    // before that iteration's closing barrier.  The body has no branches, so the compiler's vmcnt
+    // waits stay exact (they wait for the oldest ring slot only): past the last tile the refill
+    // re-reads tile nk-1 (a cache hit), and the last iteration's store fills the idle buffer.
+    // DEPTH divides nk (the config table only offers a config when K % (BK*DEPTH) == 0).
 #pragma unroll
-        for (int ks = 0; ks < BK / 32; ++ks) {
-            const int c = ks * 4 + lgrp;
-            f16x8 fw[TN], fa[TM];
+    for (int d = 0; d < DEPTH; ++d) gload(min(d, nk - 1), rra[d], rrw[d]);
+    lstore(0, rra[0], rrw[0]);
+    gload(min(DEPTH, nk - 1), rra[0], rrw[0]);
+    __syncthreads();
+    for (int kt0 = 0; kt0 < nk; kt0 += DEPTH) {
 #pragma unroll
-            for (int a = 0; a < TN; ++a) {
-                const int r = wn0 + a * 16 + lrow;
-                fw[a] = sW[cur][r * CH + swz<CH>(r, c)];
+        for (int d = 0; d < DEPTH; ++d) {
+            const int kt = kt0 + d;
+            {
+                constexpr int KS = BK / 32;
+                f16x8 fw[KS][TN], fa[KS][TM];
+                const int cur = kt & 1;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const int c = ks * 4 + lgrp;
+#pragma unroll
+                    for (int a = 0; a < TN; ++a) {
+                        const int r = wn0 + a * 16 + lrow;
+                        fw[ks][a] = sW[cur][r * CH + swz<CH>(r, c)];
+                    }
+#pragma unroll
+                    for (int b = 0; b < TM; ++b) {
+                        const int r = wm0 + b * 16 + lrow;
+                        fa[ks][b] = sA[cur][r * CH + swz<CH>(r, c)];
+                    }
+                }
+                const int nxt = (d + 1) % DEPTH;   // a constant once the d-loop is unrolled
+                lstore(cur ^ 1, rra[nxt], rrw[nxt]);
+                gload(min(kt + 1 + DEPTH, nk - 1), rra[nxt], rrw[nxt]);
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                    for (int a = 0; a < TN; ++a)
+#pragma unroll
+                        for (int b = 0; b < TM; ++b)
+                            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fw[ks][a], fa[ks][b], acc[a][b], 0, 0, 0);
+                __syncthreads();
             }
-#pragma unroll
-            for (int b = 0; b < TM; ++b) {
-                const int r = wm0 + b * 16 + lrow;
-                fa[b] = sA[cur][r * CH + swz<CH>(r, c)];
-            }
-#pragma unroll
-            for (int a = 0; a < TN; ++a)
-#pragma unroll
-                for (int b = 0; b < TM; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fw[a], fa[b], acc[a][b], 0, 0, 0);
         }
-        if (kt + 1 < nk) lstore(cur ^ 1);
-        __syncthreads();
     }
 
     // Epilogue: lane holds D[n][m] for n = nb..nb+3, m = mrow.
@@ -251,28 +293,51 @@ __global__ void k_gemm_naive(uint16_t *__restrict__ C, const uint16_t *__restric
 
 // ---------------------------------------------------------------------------- tile table
 struct GemmCfg {
-    int bn, bm;
+    int bn, bm, kmul;   // K must be a multiple of kmul (BK * DEPTH, or 8 for the guarded kernel)
     void (*fp16)(uint16_t *, const uint16_t *, const void *, const float *, const uint16_t *, int, int, int, int, int, int);
     void (*int8)(uint16_t *, const uint16_t *, const void *, const float *, const uint16_t *, int, int, int, int, int, int);
     const char *name;
 };
 
-#define G2_CFG(BN, BM, BK, WN, WM) \
-    {BN, BM, k_gemm_mfma<BN, BM, BK, WN, WM, false>, k_gemm_mfma<BN, BM, BK, WN, WM, true>, \
-     "bn" #BN "_bm" #BM "_bk" #BK "_w" #WN "x" #WM}
+#define G2_CFG(BN, BM, BK, WN, WM, D) \
+    {BN, BM, BK * D, k_gemm_mfma<BN, BM, BK, WN, WM, false, D>, k_gemm_mfma<BN, BM, BK, WN, WM, true, D>, \
+     "bn" #BN "_bm" #BM "_bk" #BK "_w" #WN "x" #WM "_d" #D}
 
 static const GemmCfg kCfgs[] = {
-    G2_CFG(128, 128, 64, 2, 2),  // 0: wave tile 64x64
-    G2_CFG(128, 64, 64, 2, 2),   // 1: wave tile 64x32
-    G2_CFG(64, 128, 64, 2, 2),   // 2: wave tile 32x64
-    G2_CFG(64, 64, 64, 2, 2),    // 3: wave tile 32x32
-    G2_CFG(128, 32, 64, 4, 1),   // 4: wave tile 32x32
-    G2_CFG(64, 32, 64, 2, 2),    // 5: wave tile 32x16
-    G2_CFG(32, 64, 64, 1, 4),    // 6: wave tile 32x16
+    G2_CFG(128, 128, 64, 2, 2, 2),  // 0: wave tile 64x64
+    G2_CFG(128, 64, 64, 2, 2, 4),   // 1: wave tile 64x32
+    G2_CFG(64, 128, 64, 2, 2, 4),   // 2: wave tile 32x64
+    G2_CFG(64, 64, 64, 2, 2, 6),    // 3: wave tile 32x32
+    G2_CFG(128, 32, 64, 4, 1, 6),   // 4: wave tile 32x32
+    G2_CFG(64, 32, 64, 2, 2, 6),    // 5: wave tile 32x16
+    G2_CFG(32, 64, 64, 1, 4, 6),    // 6: wave tile 32x16
+    G2_CFG(96, 64, 64, 2, 2, 6),    // 7: wave tile 48x32
+    G2_CFG(64, 64, 64, 2, 2, 12),   // 8: wave tile 32x32, whole K=768 in flight
+    G2_CFG(64, 32, 64, 2, 2, 12),   // 9: wave tile 32x16
+    G2_CFG(32, 32, 64, 2, 2, 12),   // 10: wave tile 16x16
+    G2_CFG(96, 32, 64, 2, 2, 6),    // 11: wave tile 48x16
+    G2_CFG(64, 64, 64, 2, 2, 1),    // 12: no prefetch ring (reference point)
+    G2_CFG(64, 64, 128, 2, 2, 3),   // 13: BK=128: half the barriers
+    G2_CFG(96, 64, 128, 2, 2, 3),   // 14
+    G2_CFG(64, 32, 128, 2, 2, 3),   // 15
+    G2_CFG(32, 64, 128, 1, 4, 3),   // 16
+    G2_CFG(64, 64, 128, 2, 2, 2),   // 17
+    G2_CFG(128, 64, 128, 2, 2, 2),  // 18
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
 
+// Any K % 8 == 0 (int8: K % 16 == 0): predicated loads, one k-tile of prefetch.
+#define G2_GCFG(BN, BM, WN, WM) \
+    {BN, BM, 8, k_gemm_mfma<BN, BM, 64, WN, WM, false, 1, true>, k_gemm_mfma<BN, BM, 64, WN, WM, true, 1, true>, \
+     "guard_bn" #BN "_bm" #BM}
+static const GemmCfg kGuardCfgs[] = {
+    G2_GCFG(64, 64, 2, 2),
+    G2_GCFG(64, 32, 2, 2),
+};
+
 static int g_force_cfg = -2;  // -2: not read yet; -1: table
+
+static bool cfg_fits(int c, int K) { return K % kCfgs[c].kmul == 0; }
 
 static int pick_cfg(int M, int N, int K) {
     if (g_force_cfg == -2) {
@@ -280,16 +345,27 @@ static int pick_cfg(int M, int N, int K) {
         g_force_cfg = e ? atoi(e) : -1;
         if (g_force_cfg >= kNumCfgs) g_force_cfg = -1;
     }
-    if (g_force_cfg >= 0) return g_force_cfg;
-    // Pick the largest tile that still gives about one work-group per CU (256 CUs).
-    const long cu = 256;
-    const int order[] = {0, 1, 2, 3, 4, 5};
-    for (int c : order) {
-        const long t = (long)cdiv(N, kCfgs[c].bn) * cdiv(M, kCfgs[c].bm);
-        if (t >= cu) return c;
+    if (g_force_cfg >= 0 && cfg_fits(g_force_cfg, K)) return g_force_cfg;
+    // Measured picks for the GPT-2 prefill shapes at M in (256, 512] (12-layer sweeps with L2-cold
+    // weights on MI355X), then a fallback: the largest tile that still gives about one work-group
+    // per CU (256 CUs), among the configs whose ring depth divides K; -1 when none does (the
+    // guarded kernel runs).
+    if (M > 256 && M <= 512) {
+        int c = -1;
+        if (N == 768 && K == 768) c = 6;          // attn-proj: 32x64, depth 6
+        else if (N == 768 && K == 3072) c = 5;    // mlp-proj: 64x32, depth 6
+        else if (N >= 2048 && K == 768) c = 7;    // QKV, fc: 96x64, depth 6
+        if (c >= 0 && cfg_fits(c, K)) return c;
     }
-    (void)K;
-    return 5;
+    const int order[] = {0, 1, 2, 7, 3, 4, 11, 5, 6, 10};
+    int last = -1;
+    for (int c : order) {
+        if (!cfg_fits(c, K)) continue;
+        last = c;
+        const long t = (long)cdiv(N, kCfgs[c].bn) * cdiv(M, kCfgs[c].bm);
+        if (t >= 256) return c;
+    }
+    return last;
 }
 
 static bool mfma_ok(const void *A, const void *W, int K, bool qw) {
@@ -297,9 +373,8 @@ static bool mfma_ok(const void *A, const void *W, int K, bool qw) {
     return (K % 8) == 0 && aligned16(A) && aligned16(W);
 }
 
-static void launch_gemm(int cfg, uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const uint16_t *bias,
-                        int M, int N, int K, bool qw) {
-    const GemmCfg &g = kCfgs[cfg];
+static void launch_gemm(const GemmCfg &g, uint16_t *C, const uint16_t *A, const void *W, const float *Ws,
+                        const uint16_t *bias, int M, int N, int K, bool qw) {
     const int tiles_m = cdiv(M, g.bm), tiles_n = cdiv(N, g.bn);
     const int ntiles = tiles_m * tiles_n;
     const int vec = (N % 4 == 0) && (((uintptr_t)C & 7u) == 0);
@@ -318,7 +393,9 @@ void gemm(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const 
     if ((long)M * N == 0) return;
     // K == 0 (an empty sum, C = bias or 0) falls through to the generic kernel.
     if (K > 0 && mfma_ok(A, W, K, qw)) {
-        launch_gemm(cfg >= 0 && cfg < kNumCfgs ? cfg : pick_cfg(M, N, K), C, A, W, Ws, bias, M, N, K, qw);
+        const int c = (cfg >= 0 && cfg < kNumCfgs && cfg_fits(cfg, K)) ? cfg : pick_cfg(M, N, K);
+        if (c >= 0) launch_gemm(kCfgs[c], C, A, W, Ws, bias, M, N, K, qw);
+        else launch_gemm(kGuardCfgs[(long)cdiv(N, 64) * cdiv(M, 64) >= 256 ? 0 : 1], C, A, W, Ws, bias, M, N, K, qw);
         check_launch(qw ? "k_gemm_mfma<int8>" : "k_gemm_mfma<fp16>");
         return;
     }
@@ -358,6 +435,9 @@ extern "C" void gpt2_matmul_naive(gpt2_half *C, const gpt2_half *A, const gpt2_h
 extern "C" int gpt2_tune_gemm_count(void) { return kNumCfgs; }
 extern "C" const char *gpt2_tune_gemm_name(int cfg) { return cfg >= 0 && cfg < kNumCfgs ? kCfgs[cfg].name : "?"; }
 extern "C" int gpt2_tune_gemm_pick(int M, int N, int K) { return pick_cfg(M, N, K); }
+extern "C" int gpt2_tune_gemm_fits(int cfg, int K) { return cfg >= 0 && cfg < kNumCfgs && cfg_fits(cfg, K); }
+// Force one config for every later GEMM whose K it accepts (-1 restores the table).
+extern "C" void gpt2_tune_gemm_force(int cfg) { g_force_cfg = (cfg >= 0 && cfg < kNumCfgs) ? cfg : -1; }
 extern "C" void gpt2_tune_gemm_run(int cfg, gpt2_half *C, const gpt2_half *A, const void *W, const float *Ws,
                                    const gpt2_half *bias, int M, int N, int K) {
     if (gemm_args("gpt2_tune_gemm_run", C, A, W, M, N, K)) return;

@@ -1,0 +1,388 @@
+#!/usr/bin/env python
+"""Benchmark of the MI355X matmul path of bare-metal-gpt2 (BASELINE.json metric).
+
+Headline (`value`): fp16 prefill GEMM TFLOP/s at P=512 -- one step is the prefill's trunk GEMM set,
+12 layers x {QKV 512x2304x768, attn-proj 512x768x768, fc 512x3072x768, mlp-proj 512x768x3072}
+(+bias), each layer with its own weights, run back to back through gpt2_matmul_tiled.  Inputs are
+resident in HBM before the timed region; timing is hipEvents on the launch stream around K steps.
+
+Also reported in the same JSON line:
+  roofline      the GEMM kernel with the largest share of the step, against 2500 TFLOP/s fp16 MFMA
+  gemv_int8     INT8 decode GEMV GB/s per trunk shape, cold (rotating > 512 MB of weight copies,
+                so every launch streams from HBM) and warm (same weights every launch), plus the
+                48-GEMV trunk chain of one decode step
+  head_gemv     fp16 tied-head GEMV (77.3 MB) cold / warm
+  decode        GPT-2-124M decode tok/s @ctx=512: INT8 trunk + fp16 head, one hipGraph replay per
+                token, after a P=512 prefill; plus the mean over the 511-step greedy run
+  cpu_baseline  the reference's own cpu/forward_cpu.c matmul (oracle/_ref, if built) or the oracle
+                restatement, on the same four GEMM shapes, on this host's cores
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "prefill GEMM TFLOP/s @P=512; INT8 decode GEMV HBM GB/s; decode tok/s @ctx=512"
+PEAK_FP16_TFLOPS = 2500.0      # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+M_PREFILL = 512
+GEMM_SET = [("qkv", 2304, 768), ("attn_proj", 768, 768), ("fc", 3072, 768), ("mlp_proj", 768, 3072)]
+TRUNK_GEMV = [("qkv", 2304, 768), ("attn_proj", 768, 768), ("fc", 3072, 768), ("mlp_proj", 768, 3072)]
+N_LAYER, VOCAB, N_EMBD = 12, 50257, 768
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Bench:
+    def __init__(self, pkg):
+        self.pkg = pkg
+        self.L = pkg.lib()
+        self.keep = []
+
+    def dev(self, a):
+        d = self.pkg.Dev.from_numpy(a)
+        self.keep.append(d)
+        return d
+
+    def empty(self, nbytes):
+        d = self.pkg.Dev(nbytes)
+        self.keep.append(d)
+        return d
+
+    def op(self, kind, Cb, A, W, Ws, bias, M, N, K):
+        return self.pkg.GPT2BenchOp(kind, Cb, A, W, Ws, bias, M, N, K)
+
+    def run_ops(self, ops, warmup, iters, per_op=False):
+        arr = (self.pkg.GPT2BenchOp * len(ops))(*ops)
+        ms = C.c_float()
+        per = (C.c_float * len(ops))() if per_op else None
+        rc = self.L.gpt2_bench_ops(arr, len(ops), warmup, iters, C.byref(ms),
+                                   C.cast(per, C.POINTER(C.c_float)) if per_op else None)
+        if rc:
+            self.pkg.check("gpt2_bench_ops")
+            raise RuntimeError(f"gpt2_bench_ops rc={rc}")
+        return ms.value, (list(per) if per_op else None)
+
+
+def f16(rng, shape, std):
+    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float16)
+
+
+# ------------------------------------------------------------------------------ prefill GEMM set
+def bench_gemm_set(B, steps, warmup):
+    rng = np.random.default_rng(1234)
+    L = B.L
+    X = B.dev(f16(rng, (M_PREFILL, 768), 1.0))
+    Xf = B.dev(f16(rng, (M_PREFILL, 3072), 1.0))
+    outs = {name: B.empty(M_PREFILL * N * 2) for name, N, K in GEMM_SET}
+    ops = []
+    for layer in range(N_LAYER):
+        for name, N, K in GEMM_SET:
+            W = B.dev(f16(rng, (N, K), 0.02))
+            b = B.dev(f16(rng, N, 0.01))
+            A = Xf if K == 3072 else X
+            ops.append(B.op(0, outs[name].ptr, A.ptr, W.ptr, None, b.ptr, M_PREFILL, N, K))
+    flops_step = sum(2.0 * M_PREFILL * N * K for _, N, K in GEMM_SET) * N_LAYER
+    ms_step, _ = B.run_ops(ops, warmup, steps)
+    # Per-kernel launch durations for the roofline, under the step's own conditions: each shape's
+    # 12 layer GEMMs (distinct weights, so the weights are not L2-resident) back to back.
+    shapes = []
+    by_cfg = {}
+    for j, (name, N, K) in enumerate(GEMM_SET):
+        ms_shape, _ = B.run_ops(ops[j::4], 3, max(20, steps // 4))
+        ms = ms_shape / N_LAYER
+        cfg = L.gpt2_tune_gemm_pick(M_PREFILL, N, K)
+        cname = L.gpt2_tune_gemm_name(cfg).decode()
+        fl = 2.0 * M_PREFILL * N * K
+        shapes.append({"gemm": name, "M": M_PREFILL, "N": N, "K": K, "kernel": cname, "us": round(ms * 1e3, 3),
+                       "tflops": round(fl / (ms * 1e-3) / 1e12, 2)})
+        c = by_cfg.setdefault(cname, {"flops": 0.0, "ms": 0.0, "launches": 0})
+        c["flops"] += fl
+        c["ms"] += ms
+        c["launches"] += 1
+    dom = max(by_cfg.items(), key=lambda kv: kv[1]["ms"])
+    d = dom[1]
+    achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": None,
+                "kernel": f"k_gemm_mfma<{dom[0]}>", "avg_launch_us": round(d["ms"] / d["launches"] * 1e3, 3),
+                "flops_per_launch": d["flops"] / d["launches"]}
+    roofline.update(measured_traffic(dom[0], [x for x in shapes if x["kernel"] == dom[0]]))
+    return flops_step, ms_step, shapes, roofline
+
+
+def measured_traffic(cfg_name, shapes):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE runs (profiles/gemm_prefill_p512_hbm_traffic.md), averaged over the shapes that kernel
+    serves in the step; null when that profile does not cover this kernel config."""
+    path = os.path.join(ROOT, "profiles", "gemm_prefill_p512_hbm_traffic.json")
+    try:
+        prof = json.load(open(path))
+    except (OSError, ValueError):
+        return {}
+    key = {(2304, 768): "QKV 512x2304x768", (3072, 768): "fc 512x3072x768", (768, 768): "attn-proj 512x768x768",
+           (768, 3072): "mlp-proj 512x768x3072"}
+    want = [prof["per_shape"].get(key.get((x["N"], x["K"]), ""), {}) for x in shapes]
+    import re
+    m = re.fullmatch(r"bn(\d+)_bm(\d+)_bk(\d+)_w(\d+)x(\d+)_d(\d+)", cfg_name)
+    if not m:
+        return {}
+    bn, bm, bk, wn, wm, dep = m.groups()
+    tag = f"k_gemm_mfma<{bn}, {bm}, {bk}, {wn}, {wm}, false, {dep}, false>"
+    if not want or any(not w or w.get("kernel") != tag for w in want):
+        return {}
+    return {"traffic": round(sum(w["bytes"] for w in want) / len(want)), "traffic_source": prof["source"]}
+
+
+# ------------------------------------------------------------------------------ INT8 / fp16 GEMVs
+def quantize_dev(B, w16_dev, N, K):
+    q = B.empty(N * K)
+    s = B.empty(N * 4)
+    B.L.gpt2_quantize_rows(q.ptr, s.ptr, w16_dev.ptr, N, K)
+    B.L.gpt2_sync()
+    B.pkg.check("quantize")
+    return q, s
+
+
+def copies_for(nbytes, floor=600e6):
+    return max(4, int(np.ceil(floor / nbytes)))
+
+
+def bench_gemv(B):
+    rng = np.random.default_rng(4321)
+    L = B.L
+    res = {}
+    x768 = B.dev(f16(rng, 768, 1.0))
+    x3072 = B.dev(f16(rng, 3072, 1.0))
+    y = B.empty(VOCAB * 2)
+    chain = []
+    for name, N, K in TRUNK_GEMV:
+        x = x3072 if K == 3072 else x768
+        w16 = B.dev(f16(rng, (N, K), 0.02))
+        q, s = quantize_dev(B, w16, N, K)
+        b = B.dev(f16(rng, N, 0.01))
+        algo = N * K + 4 * N + 2 * K + 2 * N + 2 * N
+        R = copies_for(N * K)
+        big = B.empty(R * N * K)
+        for r in range(R):
+            L.gpt2_d2d(big.at(r * N * K), q.ptr, N * K)
+        L.gpt2_sync()
+        cold_ops = [B.op(3, y.ptr, x.ptr, big.at(r * N * K), s.ptr, b.ptr, 1, N, K) for r in range(R)]
+        ms_cold, _ = B.run_ops(cold_ops, 1, 5)
+        ms_cold /= R
+        ms_warm, _ = B.run_ops([B.op(3, y.ptr, x.ptr, q.ptr, s.ptr, b.ptr, 1, N, K)], 50, 2000)
+        res[name] = {"N": N, "K": K, "bytes": algo, "copies": R,
+                     "cold_us": round(ms_cold * 1e3, 3), "cold_GBs": round(algo / (ms_cold * 1e-3) / 1e9, 1),
+                     "warm_us": round(ms_warm * 1e3, 3), "warm_GBs": round(algo / (ms_warm * 1e-3) / 1e9, 1)}
+        big.free()
+    # the 48 INT8 GEMVs of one decode step, distinct weights per layer, back to back
+    chain_bytes = 0
+    for layer in range(N_LAYER):
+        for name, N, K in TRUNK_GEMV:
+            x = x3072 if K == 3072 else x768
+            q = B.dev(rng.integers(-127, 128, (N, K), dtype=np.int8))
+            s = B.dev(np.full(N, 1e-3, np.float32))
+            b = B.dev(f16(rng, N, 0.01))
+            chain.append(B.op(3, y.ptr, x.ptr, q.ptr, s.ptr, b.ptr, 1, N, K))
+            chain_bytes += N * K + 4 * N + 2 * K + 4 * N
+    ms_chain, _ = B.run_ops(chain, 20, 200)
+    res["trunk_chain_48"] = {"bytes": chain_bytes, "us": round(ms_chain * 1e3, 2),
+                             "GBs": round(chain_bytes / (ms_chain * 1e-3) / 1e9, 1)}
+    # fp16 tied head: [1x768] . [768x50257], 77.3 MB
+    N, K = VOCAB, 768
+    algo = 2 * N * K + 2 * K + 2 * N
+    R = 4
+    big = B.empty(R * N * K * 2)
+    head = f16(rng, (N, K), 0.02)
+    for r in range(R):
+        L.gpt2_h2d(big.at(r * N * K * 2), head.ctypes.data, head.nbytes)
+    ms_cold, _ = B.run_ops([B.op(2, y.ptr, x768.ptr, big.at(r * N * K * 2), None, None, 1, N, K) for r in range(R)], 1, 10)
+    ms_cold /= R
+    ms_warm, _ = B.run_ops([B.op(2, y.ptr, x768.ptr, big.ptr, None, None, 1, N, K)], 10, 200)
+    head_res = {"N": N, "K": K, "bytes": algo, "cold_us": round(ms_cold * 1e3, 2),
+                "cold_GBs": round(algo / (ms_cold * 1e-3) / 1e9, 1), "warm_us": round(ms_warm * 1e3, 2),
+                "warm_GBs": round(algo / (ms_warm * 1e-3) / 1e9, 1)}
+    big.free()
+    return res, head_res
+
+
+# ------------------------------------------------------------------------------ decode (config 5)
+def bench_decode(B, steady_reps=64):
+    import importlib
+    pkg, L = B.pkg, B.L
+    synth = importlib.import_module("bare_metal_gpt2_amd.synth")
+    t0 = time.time()
+    body = synth.make_body(seed=1234, plain=True)
+    model = pkg.Model(body)
+    del body
+    model.quantize()                       # 48 trunk tensors INT8, head fp16
+    kv = pkg.KVCache(1024)
+    scr = pkg.Scratch(1024)
+    P = 512
+    ids = synth.token_ids(P, seed=1234)
+    d_ids = B.dev(ids)
+    logits = B.empty(VOCAB * 2)
+    tokens = B.empty(1024 * 4)
+    be = pkg.backend("int8")
+    caps = pkg.GPT2CapsGPU()
+    caps.logits = logits.ptr
+    caps.logits_all = 0
+    L.gpt2_prefill_fill_cache(be, C.byref(model.gpu), C.byref(kv.kv), d_ids.ptr, P, C.byref(scr.s), C.byref(caps))
+    L.gpt2_sync()
+    pkg.check("prefill")
+    first = int(np.argmax(pkg.half_bits_to_f32(logits.numpy(np.uint16, (VOCAB,)))))
+    g = L.gpt2_decode_graph_create(be, C.byref(model.gpu), C.byref(kv.kv), C.byref(scr.s), logits.ptr, tokens.ptr)
+    if not g:
+        pkg.check("graph create")
+        raise RuntimeError("graph create failed")
+    ms = C.c_float()
+    # steady state at pos 512 (cache length 512): each replay is re-pinned to pos 512
+    samples = []
+    for i in range(steady_reps + 5):
+        L.gpt2_decode_graph_set(g, first, P)
+        L.gpt2_decode_graph_time(g, 1, C.byref(ms))
+        if i >= 5:
+            samples.append(ms.value)
+    pkg.check("steady decode")
+    # eager (non-graph) step at the same position, for the launch-overhead comparison
+    eager = []
+    for i in range(12):
+        kv.kv.len = P
+        L.gpt2_sync()
+        t = time.perf_counter()
+        L.gpt2_decode_step_cuda(be, C.byref(model.gpu), C.byref(kv.kv), first, P, C.byref(scr.s), logits.ptr, None)
+        L.gpt2_sync()
+        if i >= 2:
+            eager.append((time.perf_counter() - t) * 1e3)
+    pkg.check("eager decode")
+    # the full greedy run: 511 steps from pos 512 (ctx 512 -> 1023)
+    L.gpt2_decode_graph_set(g, first, P)
+    L.gpt2_decode_graph_time(g, 511, C.byref(ms))
+    tok, pos = C.c_int(), C.c_int()
+    L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos))
+    pkg.check("greedy run")
+    L.gpt2_decode_graph_destroy(g)
+    streamed = model.q.streamed_bytes
+    kv_bytes = L.gpt2_kv_step_bytes(C.byref(kv.kv), P + 1)
+    med = float(np.median(samples))
+    res = {"tok_s_at_512": round(1000.0 / med, 1), "ms_step_at_512": round(med, 4),
+           "ms_step_min_max": [round(min(samples), 4), round(max(samples), 4)],
+           "eager_ms_step_at_512": round(float(np.median(eager)), 4),
+           "greedy_511_tok_s": round(1000.0 / ms.value, 1), "greedy_final_pos": pos.value,
+           "weight_bytes": int(streamed), "kv_bytes_at_513": int(kv_bytes),
+           "step_GBs_at_512": round((streamed + kv_bytes) / (med * 1e-3) / 1e9, 1),
+           "setup_s": round(time.time() - t0, 1)}
+    scr.free()
+    kv.free()
+    model.free()
+    return res
+
+
+# ------------------------------------------------------------------------------ CPU baseline
+def cpu_baseline(budget_s=12.0):
+    import oracle
+    threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
+    rng = np.random.default_rng(99)
+    use_ref = oracle.ref_available()
+    mm = oracle.ref_matmul if use_ref else oracle.matmul
+    X = rng.standard_normal((M_PREFILL, 768), dtype=np.float32)
+    Xf = rng.standard_normal((M_PREFILL, 3072), dtype=np.float32)
+    Ws = [(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02), rng.standard_normal(N, dtype=np.float32))
+          for _, N, K in GEMM_SET]
+    flops = 0.0
+    t0 = time.perf_counter()
+    sets = 0
+    while True:
+        for (name, N, K), (W, b) in zip(GEMM_SET, Ws):
+            mm(Xf if K == 3072 else X, W, b)
+            flops += 2.0 * M_PREFILL * N * K
+        sets += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "reference" if use_ref else "port",
+            "sample": f"{sets} x the 4-GEMM set at M=512 (one layer of the workload, {flops / sets / 1e9:.3f} GFLOP"
+                      f" per set), fp32 storage / double accumulation, {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="only the headline GEMM set")
+    ap.add_argument("--no-decode", action="store_true", help="skip the graph-replayed decode leg")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="also run one plain copy of BYTES (calibrates FETCH_SIZE/WRITE_SIZE counters)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the matmul path "
+              "would shard by output rows (see DESIGN.md), but no multi-GPU run is part of it.", file=sys.stderr)
+        sys.exit(2)
+    cpu_threads = max(1, min(16, os.cpu_count() or 1))
+    os.environ.setdefault("OMP_NUM_THREADS", str(cpu_threads))
+
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    L = pkg.lib()
+    cus, clk = C.c_int(), C.c_int()
+    name = C.create_string_buffer(256)
+    if L.gpt2_device_info(C.byref(cus), C.byref(clk), name, 256):
+        raise SystemExit("no HIP device visible")
+    B = Bench(pkg)
+    log(f"device {name.value.decode()} CUs={cus.value} clock={clk.value / 1e3:.0f} MHz")
+
+    if args.copy_probe:
+        src, dst = pkg.Dev(args.copy_probe), pkg.Dev(args.copy_probe)
+        L.gpt2_memset(src.ptr, 1, args.copy_probe)
+        ms = C.c_float()
+        L.gpt2_bench_copy(dst.ptr, src.ptr, args.copy_probe, C.byref(ms))
+        log(f"copy probe: {args.copy_probe} B in {ms.value * 1e3:.1f} us")
+        src.free()
+        dst.free()
+    flops_step, ms_step, shapes, roofline = bench_gemm_set(B, args.steps, args.warmup)
+    value = flops_step / (ms_step * 1e-3) / 1e12
+    log(f"prefill GEMM set: {ms_step * 1e3:.1f} us/step -> {value:.1f} TFLOP/s; per shape {shapes}")
+    out = {"metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+           "config": {"workload": "prefill trunk GEMM set @P=512: 12 layers x {QKV 512x2304x768, attn-proj "
+                                  "512x768x768, fc 512x3072x768, mlp-proj 512x768x3072} + bias, fp16 in, fp32 acc, "
+                                  "fp16 out (BASELINE config 2, per layer)",
+                      "M": M_PREFILL, "layers": N_LAYER, "gflop_per_step": round(flops_step / 1e9, 4),
+                      "device": name.value.decode()},
+           "roofline": roofline, "gemm_shapes": shapes}
+    B.keep.clear()
+    if not args.no_extras:
+        gemv, head = bench_gemv(B)
+        B.keep.clear()
+        log(f"gemv: {gemv}\nhead: {head}")
+        out["gemv_int8"] = gemv
+        out["head_gemv_fp16"] = head
+        if not args.no_decode:
+            out["decode"] = bench_decode(B)
+            B.keep.clear()
+            log(f"decode: {out['decode']}")
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline()
+        log(f"cpu: {out['cpu_baseline']}")
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,286 @@
+"""Whole-model parity: the prefill forward, the M=1 decode step and the graph-replayed greedy loop.
+
+Gates follow the reference's own (QUALITY_GATES.md, bench/correctness_cuda.cu:70-75,200-219,
+bench/kv_gate.cu:114-138), applied to the fp16 engine against the fp32 CPU oracle:
+  rel_err = max|got - ref| / max|ref| <= 1e-2 per captured stage (gate (a), fp16 bound),
+  max KL(softmax(ref) || softmax(got)) < 0.02 over the logits rows (gate (c)),
+  cached decode == no-KV recompute within fp16 noise (the [EQ] gate).
+INT8 runs are compared with the oracle on the dequantized weights (tools/dequant_check.py).
+The graph-replayed decode uses the same kernels in the same order as the eager step, so its tokens
+and logits must match the eager loop bit for bit.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+V, E = 50257, 768
+
+
+def rel_err(got, ref):
+    return float(np.abs(got.astype(np.float64) - ref).max() / (np.abs(ref).max() + 1e-9))
+
+
+def kl_rows(ref, got):
+    def logsm(x):
+        x = x.astype(np.float64)
+        m = x.max(axis=-1, keepdims=True)
+        return x - m - np.log(np.exp(x - m).sum(axis=-1, keepdims=True))
+    lr, lg = logsm(ref), logsm(got)
+    return (np.exp(lr) * (lr - lg)).sum(axis=-1)
+
+
+@pytest.fixture(scope="module")
+def body(synth):
+    return synth.make_body(seed=555, plain=False)
+
+
+@pytest.fixture(scope="module")
+def model(pkg, body):
+    m = pkg.Model(body)
+    yield m
+    m.free()
+
+
+@pytest.fixture(scope="module")
+def deq_body(synth, body):
+    """The fp32 body with every trunk matrix replaced by fl32(q*s) of its fp16 view (head kept)."""
+    out = body.copy()
+    off = synth.offsets()
+    for Lyr in range(12):
+        for name in ("qkv_w", "attn_proj_w", "fc_w", "proj_w"):
+            o, shape = off[f"h{Lyr}.{name}"]
+            q, s, _ = oracle.quantize_fp16_view(body[o:o + int(np.prod(shape))].reshape(shape))
+            out[o:o + int(np.prod(shape))] = oracle.dequantize(q, s).reshape(-1)
+    return out
+
+
+def gpu_forward(pkg, L, model, ids, backend="flash", logits_all=True, want_blocks=False):
+    T = len(ids)
+    scr = pkg.Scratch(T)
+    d_ids = pkg.Dev.from_numpy(np.asarray(ids, np.int32))
+    logits = pkg.Dev((T if logits_all else 1) * V * 2)
+    blocks = pkg.Dev(12 * T * E * 2) if want_blocks else None
+    fin = pkg.Dev(T * E * 2)
+    caps = pkg.GPT2CapsGPU()
+    caps.logits, caps.logits_all, caps.final_ln = logits.ptr, int(logits_all), fin.ptr
+    if blocks is not None:
+        caps.blocks = blocks.ptr
+    L.gpt2_forward_cuda(pkg.backend(backend), C.byref(model.gpu), d_ids.ptr, T, C.byref(scr.s), C.byref(caps))
+    L.gpt2_sync()
+    pkg.check("forward")
+    out = {"logits": oracle.f16_to_f32(logits.numpy(np.uint16, ((T if logits_all else 1), V))),
+           "final_ln": oracle.f16_to_f32(fin.numpy(np.uint16, (T, E)))}
+    if blocks is not None:
+        out["blocks"] = oracle.f16_to_f32(blocks.numpy(np.uint16, (12, T, E)))
+    scr.free()
+    return out
+
+
+def test_prefill_forward_fp16(pkg, L, synth, body, model):
+    ids = synth.token_ids(24, seed=1)
+    got = gpu_forward(pkg, L, model, ids, "flash", want_blocks=True)
+    ref = oracle.forward(oracle.fp16_view(body), ids, logits_all=True, want_blocks=True)
+    for Lyr in range(12):
+        assert rel_err(got["blocks"][Lyr], ref["blocks"][Lyr]) <= 1e-2, Lyr
+    assert rel_err(got["final_ln"], ref["final_ln"]) <= 1e-2
+    assert rel_err(got["logits"], ref["logits"]) <= 1e-2
+    assert kl_rows(ref["logits"], got["logits"]).max() < 0.02
+    assert (got["logits"].argmax(-1) == ref["logits"].argmax(-1)).mean() >= 0.95
+
+
+def test_config1_forward_t64(pkg, L, synth):
+    """plain model (biases 0, LN 1/0), 64 random ids, logits [64 x 50257]."""
+    b = synth.make_body(seed=1234, plain=True)
+    m = pkg.Model(b)
+    try:
+        ids = synth.token_ids(64, seed=1234)
+        got = gpu_forward(pkg, L, m, ids, "flash")
+        ref = oracle.forward(oracle.fp16_view(b), ids, logits_all=True)
+        assert rel_err(got["logits"], ref["logits"]) <= 1e-2
+        assert kl_rows(ref["logits"], got["logits"]).max() < 0.02
+    finally:
+        m.free()
+
+
+def test_prefill_forward_backends_agree(pkg, L, synth, model):
+    ids = synth.token_ids(17, seed=2)
+    outs = {be: gpu_forward(pkg, L, model, ids, be)["logits"] for be in ("naive", "tiled", "flash", "gemv")}
+    for be in ("naive", "tiled", "gemv"):
+        assert rel_err(outs[be], outs["flash"]) <= 5e-3, be
+
+
+def test_prefill_forward_int8(pkg, L, synth, body, model, deq_body):
+    ids = synth.token_ids(20, seed=3)
+    model.quantize()
+    try:
+        got = gpu_forward(pkg, L, model, ids, "int8")
+    finally:
+        L.gpt2_quant_free(C.byref(model.q))
+        model.q = None
+        model.gpu.q = None
+    ref = oracle.forward(oracle.fp16_view(deq_body), ids, logits_all=True)
+    assert rel_err(got["final_ln"], ref["final_ln"]) <= 1e-2
+    assert rel_err(got["logits"], ref["logits"]) <= 1e-2
+    assert kl_rows(ref["logits"], got["logits"]).max() < 0.02
+
+
+def test_last_row_logits(pkg, L, synth, model):
+    ids = synth.token_ids(33, seed=4)
+    full = gpu_forward(pkg, L, model, ids, "flash", logits_all=True)["logits"]
+    last = gpu_forward(pkg, L, model, ids, "flash", logits_all=False)["logits"]
+    assert rel_err(last[0], full[-1]) <= 2e-3
+
+
+def decode_setup(pkg, L, model, ids, backend):
+    P = len(ids)
+    kv = pkg.KVCache(1024)
+    scr = pkg.Scratch(1024)
+    d_ids = pkg.Dev.from_numpy(np.asarray(ids, np.int32))
+    logits = pkg.Dev(V * 2)
+    caps = pkg.GPT2CapsGPU()
+    caps.logits, caps.logits_all = logits.ptr, 0
+    L.gpt2_prefill_fill_cache(pkg.backend(backend), C.byref(model.gpu), C.byref(kv.kv), d_ids.ptr, P,
+                              C.byref(scr.s), C.byref(caps))
+    L.gpt2_sync()
+    pkg.check("prefill_fill_cache")
+    assert kv.kv.len == P
+    return kv, scr, logits
+
+
+@pytest.mark.parametrize("backend", ["gemv", "int8", "flash"])
+def test_decode_matches_recompute(pkg, L, synth, model, backend):
+    """[EQ]: logits of cached M=1 steps == last-row logits of a full forward over the sequence."""
+    if backend == "int8":
+        model.quantize()
+    try:
+        ids = list(synth.token_ids(40, seed=5))
+        P = 32
+        kv, scr, logits = decode_setup(pkg, L, model, ids[:P], backend)
+        be = pkg.backend(backend)
+        caps = pkg.Dev(14 * E * 2)
+        for pos in range(P, len(ids)):
+            L.gpt2_decode_step_cuda(be, C.byref(model.gpu), C.byref(kv.kv), int(ids[pos]), pos, C.byref(scr.s),
+                                    logits.ptr, caps.ptr)
+            L.gpt2_sync()
+            pkg.check("decode step")
+            assert kv.kv.len == pos + 1
+            got = oracle.f16_to_f32(logits.numpy(np.uint16, (1, V)))
+            ref = gpu_forward(pkg, L, model, ids[:pos + 1], backend, logits_all=False)["logits"]
+            assert kl_rows(ref, got).max() < 0.02
+            assert rel_err(got, ref) <= 1e-2
+            assert got.argmax() == ref.argmax()
+        scr.free()
+        kv.free()
+    finally:
+        if backend == "int8":
+            L.gpt2_quant_free(C.byref(model.q))
+            model.q = None
+            model.gpu.q = None
+
+
+def test_decode_vs_oracle(pkg, L, synth, body, model):
+    """Decode-only run from position 0 (cache filled entirely by M=1 steps) against the oracle."""
+    ids = synth.token_ids(12, seed=6)
+    kv = pkg.KVCache(64)
+    scr = pkg.Scratch(64)
+    logits = pkg.Dev(V * 2)
+    be = pkg.backend("gemv")
+    try:
+        for pos, tok in enumerate(ids):
+            L.gpt2_decode_step_cuda(be, C.byref(model.gpu), C.byref(kv.kv), int(tok), pos, C.byref(scr.s),
+                                    logits.ptr, None)
+        L.gpt2_sync()
+        pkg.check("decode")
+        got = oracle.f16_to_f32(logits.numpy(np.uint16, (1, V)))
+        ref = oracle.forward(oracle.fp16_view(body), ids, logits_all=False)["logits"]
+        assert rel_err(got, ref) <= 1e-2
+        assert kl_rows(ref, got).max() < 0.02
+    finally:
+        scr.free()
+        kv.free()
+
+
+def test_decode_rejects_bad_position(pkg, L, model):
+    kv = pkg.KVCache(8)
+    scr = pkg.Scratch(8)
+    logits = pkg.Dev(V * 2)
+    L.gpt2_last_error()
+    try:
+        L.gpt2_decode_step_cuda(pkg.backend("gemv"), C.byref(model.gpu), C.byref(kv.kv), 5, 3, C.byref(scr.s),
+                                logits.ptr, None)   # pos 3 > kv.len 0
+        assert L.gpt2_last_error() != 0
+        assert kv.kv.len == 0
+    finally:
+        scr.free()
+        kv.free()
+
+
+def eager_greedy(pkg, L, model, kv, scr, logits, backend, first, P, n):
+    be = pkg.backend(backend)
+    toks, tok = [], first
+    rows = []
+    for i in range(n):
+        L.gpt2_decode_step_cuda(be, C.byref(model.gpu), C.byref(kv.kv), int(tok), P + i, C.byref(scr.s),
+                                logits.ptr, None)
+        lg = logits.numpy(np.uint16, (V,))
+        rows.append(lg)
+        tok = int(np.argmax(oracle.f16_to_f32(lg)))   # numpy argmax keeps the first maximum
+        toks.append(tok)
+    pkg.check("eager greedy")
+    return toks, rows
+
+
+@pytest.mark.parametrize("backend", ["int8", "gemv"])
+def test_graph_decode_matches_eager(pkg, L, synth, model, backend):
+    if backend == "int8":
+        model.quantize()
+    try:
+        ids = synth.token_ids(48, seed=8)
+        P, n = len(ids), 24
+        kv, scr, logits = decode_setup(pkg, L, model, ids, backend)
+        first = int(np.argmax(oracle.f16_to_f32(logits.numpy(np.uint16, (V,)))))
+        eager_toks, eager_rows = eager_greedy(pkg, L, model, kv, scr, logits, backend, first, P, n)
+        # graph: same cache prefix (positions >= P are rewritten by the replays)
+        kv.kv.len = P
+        tokens = pkg.Dev(1024 * 4)
+        g = L.gpt2_decode_graph_create(pkg.backend(backend), C.byref(model.gpu), C.byref(kv.kv), C.byref(scr.s),
+                                       logits.ptr, tokens.ptr)
+        assert g, pkg.check("graph create")
+        try:
+            assert L.gpt2_decode_graph_set(g, first, P) == 0
+            # replay one step at a time, with unrelated eager work and syncs between replays
+            junk_a, junk_c = pkg.Dev(64 * 768 * 2), pkg.Dev(64 * 2304 * 2)
+            for i in range(n):
+                assert L.gpt2_decode_graph_run(g, 1) == 0
+                L.gpt2_matmul_tiled(junk_c.ptr, junk_a.ptr, model.gpu.layers[0].qkv_w, None, 64, 2304, 768)
+                tok, pos = C.c_int(), C.c_int()
+                assert L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)) == 0
+                assert pos.value == P + i + 1
+                assert tok.value == eager_toks[i], i
+                assert np.array_equal(logits.numpy(np.uint16, (V,)), eager_rows[i]), i
+            toks = tokens.numpy(np.int32, (1024,))
+            assert list(toks[P + 1:P + 1 + n]) == eager_toks
+            # back-to-back replays from the same start reproduce the run
+            assert L.gpt2_decode_graph_set(g, first, P) == 0
+            assert L.gpt2_decode_graph_run(g, n) == 0
+            assert L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)) == 0
+            assert pos.value == P + n and tok.value == eager_toks[-1]
+            assert kv.kv.len == P + n
+            # replays past the cache are refused
+            assert L.gpt2_decode_graph_run(g, 1024) != 0
+            L.gpt2_last_error()
+        finally:
+            L.gpt2_decode_graph_destroy(g)
+        pkg.check("graph")
+        scr.free()
+        kv.free()
+    finally:
+        if backend == "int8":
+            L.gpt2_quant_free(C.byref(model.q))
+            model.q = None
+            model.gpu.q = None

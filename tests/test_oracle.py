@@ -1,0 +1,291 @@
+"""Pins the CPU oracle before it is trusted as the parity reference.
+
+Each oracle function is checked against (1) the reference's own cpu/forward_cpu.c compiled from
+/root/reference into oracle/_ref (bit-exact; skipped where that build is absent), (2) golden vectors
+written from that build and from tools/quantize.py (tests/golden/), and (3) what the mathematics
+fixes, chosen so that a dropped term, a wrong index or a transposed operand fails.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+need_ref = pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built (no /root/reference)")
+
+
+@pytest.fixture(scope="module")
+def gold():
+    return np.load(os.path.join(GOLD, "ref_vectors.npz"))
+
+
+# ------------------------------------------------------------------ matmul (cpu/forward_cpu.c:35-50)
+def test_matmul_golden(gold):
+    for i in range(3):
+        b = gold[f"mm{i}_b"] if f"mm{i}_b" in gold else None
+        C = oracle.matmul(gold[f"mm{i}_A"], gold[f"mm{i}_W"], b)
+        assert np.array_equal(C, gold[f"mm{i}_C"]), i
+
+
+@need_ref
+@pytest.mark.parametrize("M,N,K,bias", [(1, 1, 1, True), (7, 13, 768, True), (33, 65, 3072, False),
+                                        (64, 2304, 768, True)])
+def test_matmul_vs_reference_build(M, N, K, bias):
+    rng = np.random.default_rng(M + N + K)
+    A = rng.standard_normal((M, K), dtype=np.float32)
+    W = rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+    b = rng.standard_normal(N, dtype=np.float32) if bias else None
+    assert np.array_equal(oracle.matmul(A, W, b), oracle.ref_matmul(A, W, b))
+
+
+def test_matmul_one_hot_selects_weight_row():
+    """A = e_k rows: C[m, n] = fl32(b[n] + W[n, k]); a transposed operand would pick W[k, n]."""
+    rng = np.random.default_rng(1)
+    M, N, K = 9, 11, 13
+    W = rng.standard_normal((N, K), dtype=np.float32)
+    b = rng.standard_normal(N, dtype=np.float32)
+    ks = rng.integers(0, K, M)
+    A = np.zeros((M, K), np.float32)
+    A[np.arange(M), ks] = 1.0
+    C = oracle.matmul(A, W, b)
+    expect = (b.astype(np.float64)[None, :] + W.astype(np.float64)[:, ks].T).astype(np.float32)
+    assert np.array_equal(C, expect)
+    assert np.array_equal(oracle.matmul(np.zeros((M, K), np.float32), W, b), np.tile(b, (M, 1)))
+
+
+def test_matmul_small_integers_exact():
+    rng = np.random.default_rng(2)
+    A = rng.integers(-5, 6, (17, 300)).astype(np.float32)
+    W = rng.integers(-5, 6, (23, 300)).astype(np.float32)
+    b = rng.integers(-9, 10, 23).astype(np.float32)
+    exact = A.astype(np.int64) @ W.astype(np.int64).T + b.astype(np.int64)
+    assert np.array_equal(oracle.matmul(A, W, b), exact.astype(np.float32))
+
+
+def test_matmul_against_float64_blas():
+    rng = np.random.default_rng(3)
+    A = rng.standard_normal((40, 3072), dtype=np.float32)
+    W = rng.standard_normal((50, 3072), dtype=np.float32)
+    b = rng.standard_normal(50, dtype=np.float32)
+    ref = A.astype(np.float64) @ W.astype(np.float64).T + b
+    got = oracle.matmul(A, W, b)
+    assert np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max()
+    assert not np.allclose(got, oracle.matmul(A, W), atol=1e-3)   # the bias term is present
+
+
+# ------------------------------------------------------------------ LayerNorm (cpu/forward_cpu.c:53-71)
+def test_layernorm_golden(gold):
+    assert np.array_equal(oracle.layernorm(gold["ln_x"], gold["ln_g"], gold["ln_b"]), gold["ln_y"])
+
+
+@need_ref
+def test_layernorm_vs_reference_build():
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((33, 768), dtype=np.float32) * np.float32(4) - np.float32(1)
+    g = rng.standard_normal(768, dtype=np.float32)
+    b = rng.standard_normal(768, dtype=np.float32)
+    assert np.array_equal(oracle.layernorm(x, g, b), oracle.ref_layernorm(x, g, b))
+
+
+def test_layernorm_closed_forms():
+    E = 768
+    g = np.linspace(0.5, 1.5, E).astype(np.float32)
+    b = np.linspace(-1, 1, E).astype(np.float32)
+    # constant row: x - mean = 0 exactly, so the output is the shift
+    assert np.array_equal(oracle.layernorm(np.full((1, E), 3.25, np.float32), g, b)[0], b)
+    # +-a alternating: mean 0, biased variance a^2 -> +-a / sqrt(a^2 + eps)
+    a = 2.0
+    x = np.tile(np.array([a, -a], np.float32), E // 2)[None, :]
+    eps = float(np.float32(1e-5))
+    expect = (x[0].astype(np.float64) / np.sqrt(a * a + eps)) * g + b
+    assert np.abs(oracle.layernorm(x, g, b)[0] - expect).max() < 1e-6
+    # an unbiased variance (/(E-1)) or eps outside the sqrt would fail this
+    y = oracle.layernorm(x, np.ones(E, np.float32), np.zeros(E, np.float32))[0]
+    assert abs(float(y[0]) - a / np.sqrt(a * a + eps)) < 1e-7
+
+
+# ------------------------------------------------------------------ gelu_new (cpu/forward_cpu.c:74-78)
+def test_gelu_golden(gold):
+    assert np.array_equal(oracle.gelu(gold["gelu_x"]), gold["gelu_y"])
+
+
+def test_gelu_sigmoid_identity():
+    """0.5 (1 + tanh z) = sigmoid(2z): an independent form of gelu_new."""
+    x = np.linspace(-10, 10, 4001).astype(np.float64)
+    z = np.sqrt(2 / np.pi) * (x + 0.044715 * x ** 3)
+    expect = x / (1 + np.exp(-2 * z))
+    got = oracle.gelu(x.astype(np.float32)).astype(np.float64)
+    assert np.abs(got - expect).max() <= 2e-6 * np.maximum(np.abs(expect), 1).max()
+    assert oracle.gelu(np.float32([0.0]))[0] == 0.0
+    # the cubic term matters: dropping it changes gelu(2) by ~0.005
+    exact_erfless = 2.0 / (1 + np.exp(-2 * np.sqrt(2 / np.pi) * 2.0))
+    assert abs(float(oracle.gelu(np.float32([2.0]))[0]) - exact_erfless) > 1e-3
+
+
+# ------------------------------------------------------------------ attention (cpu/forward_cpu.c:83-116)
+def test_attention_golden(gold):
+    assert np.array_equal(oracle.attention(gold["attn_qkv"]), gold["attn_y"])
+
+
+@need_ref
+def test_attention_vs_reference_build():
+    rng = np.random.default_rng(5)
+    qkv = rng.standard_normal((70, 2304), dtype=np.float32) * np.float32(2)
+    assert np.array_equal(oracle.attention(qkv), oracle.ref_attention(qkv))
+
+
+def attention_f64(qkv):
+    T = qkv.shape[0]
+    q = qkv[:, :768].reshape(T, 12, 64).astype(np.float64)
+    k = qkv[:, 768:1536].reshape(T, 12, 64).astype(np.float64)
+    v = qkv[:, 1536:].reshape(T, 12, 64).astype(np.float64)
+    s = np.einsum("ihd,jhd->hij", q, k) / 8.0
+    s = np.where(np.tril(np.ones((T, T), bool))[None], s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    return np.einsum("hij,jhd->ihd", p, v).reshape(T, 768)
+
+
+def test_attention_closed_forms():
+    rng = np.random.default_rng(6)
+    qkv = rng.standard_normal((23, 2304), dtype=np.float32)
+    out = oracle.attention(qkv)
+    assert np.abs(out - attention_f64(qkv)).max() < 1e-6
+    assert np.array_equal(out[0], qkv[0, 1536:])                 # T=1 row: softmax of one key
+    eq = qkv.copy()
+    eq[:, 768:1536] = eq[0, 768:1536]                            # equal keys: plain mean of values
+    out = oracle.attention(eq)
+    mean = np.cumsum(eq[:, 1536:].astype(np.float64), 0) / np.arange(1, 24)[:, None]
+    assert np.abs(out - mean).max() < 1e-6
+    fut = qkv.copy()
+    fut[10:] = 0                                                 # causality: rows < 10 unchanged
+    assert np.array_equal(oracle.attention(fut)[:10], oracle.attention(qkv)[:10])
+
+
+# ------------------------------------------------------------------ forward (cpu/forward_cpu.c:118-166)
+@pytest.fixture(scope="module")
+def fwd_body():
+    import __graft_entry__
+    __graft_entry__.load_package()
+    import importlib
+    synth = importlib.import_module("bare_metal_gpt2_amd.synth")
+    return synth, synth.make_body(seed=int(np.load(os.path.join(GOLD, "ref_vectors.npz"))["fwd_seed"][0]), plain=False)
+
+
+def test_forward_golden(gold, fwd_body):
+    synth, body = fwd_body
+    out = oracle.forward(body, gold["fwd_ids"], logits_all=True)
+    assert np.array_equal(out["final_ln"], gold["fwd_final_ln"])
+    assert np.array_equal(out["logits"][:, gold["fwd_logit_cols"]], gold["fwd_logits"])
+
+
+def test_weight_order_matches_reference_loader(gold):
+    """or_bind_weights hands out the same tensor offsets as model/weights.c's loader."""
+    assert np.array_equal(oracle.oracle_offsets(), gold["ref_offsets"])
+
+
+@need_ref
+def test_forward_vs_reference_build(fwd_body, gold):
+    synth, body = fwd_body
+    ids = np.array([5, 50256, 17, 900, 33333], np.int32)
+    a = oracle.forward(body, ids, logits_all=True, want_blocks=True)
+    b = oracle.ref_forward(body, gold["ref_offsets"], ids, logits_all=True, want_blocks=True)
+    for k in ("embed", "blocks", "final_ln", "logits"):
+        assert np.array_equal(a[k], b[k]), k
+    a1 = oracle.forward(body, ids, logits_all=False)
+    assert np.array_equal(a1["logits"][0], a["logits"][-1])
+
+
+# ------------------------------------------------------------------ fp16 conversion
+def test_f32_to_f16_exhaustive_against_f16c():
+    import ctypes
+    first = ctypes.c_uint32()
+    bad = oracle.lib().or_check_f16c_range(0, 1 << 32, ctypes.byref(first))
+    assert bad == 0, hex(first.value)
+    assert oracle.lib().or_check_f16c_back() == 0
+
+
+def test_f16_round_trip_and_ties():
+    h = np.arange(65536, dtype=np.uint16)
+    f = oracle.f16_to_f32(h)
+    ok = ~np.isnan(f)
+    assert np.array_equal(oracle.f32_to_f16(f[ok]), h[ok])
+    # halfway cases round to even: 1 + 2^-11 -> 1.0, 1 + 3*2^-11 -> 1 + 2^-9
+    x = np.array([1 + 2 ** -11, 1 + 3 * 2 ** -11, 65520.0, 65519.0, 2 ** -25, 3 * 2 ** -26], np.float32)
+    assert list(oracle.f16_to_f32(oracle.f32_to_f16(x))) == [1.0, 1 + 2 ** -9, np.inf, 65504.0, 0.0, 2 ** -24]
+
+
+# ------------------------------------------------------------------ INT8 scheme (tools/quantize.py:58-73)
+def test_quantizer_golden_from_reference_quantize_py():
+    g = np.load(os.path.join(GOLD, "quant_golden.npz"))
+    for case in ("rand", "special"):
+        q, s, _ = oracle.quantize_rows(g[f"{case}_w16"])
+        assert np.array_equal(q, g[f"{case}_q"]), case
+        assert np.array_equal(s.view(np.uint32), g[f"{case}_s"].view(np.uint32)), case
+
+
+def test_quantizer_invariants():
+    rng = np.random.default_rng(7)
+    w = oracle.fp16_view(rng.standard_normal((300, 768), dtype=np.float32) * np.float32(0.02))
+    w[5] = 0.0
+    q, s, dead = oracle.quantize_rows(w)
+    assert dead == 1 and s[5] == 1.0 and not q[5].any()
+    assert np.abs(q.astype(np.int32)).max() <= 127
+    live = np.ones(300, bool)
+    live[5] = False
+    assert np.all(np.abs(q[live].astype(np.int32)).max(axis=1) == 127)   # the absmax element maps to 127
+    q2, s2, _ = oracle.quantize_rows(-w)                                  # odd symmetry
+    assert np.array_equal(q2, -q) and np.array_equal(s2, s)
+    assert np.array_equal(s, np.where(np.abs(w).max(1) == 0, 1.0, np.abs(w).max(1) / np.float32(127)).astype(np.float32))
+    q3, s3, _ = oracle.quantize_rows(w * np.float32(2 ** -6))             # power-of-two scaling
+    assert np.array_equal(q3, q) and np.array_equal(s3[live], s[live] * np.float32(2 ** -6))
+
+
+def test_quantizer_ties_round_half_even():
+    w = np.zeros((2, 8), np.float32)
+    w[0, :7] = [127, 2.5, 3.5, -2.5, -3.5, 0.5, 126.5]                    # s = 1: exact ties
+    w[1, :4] = np.array([127, 2.5, -1.5, 0.5], np.float32) / 128          # s = 2^-7
+    q, s, _ = oracle.quantize_rows(w)
+    assert s[0] == 1.0 and s[1] == np.float32(1 / 128)
+    assert list(q[0, :7]) == [127, 2, 4, -2, -4, 0, 126]
+    assert list(q[1, :4]) == [127, 2, -2, 0]
+
+
+def test_quantizer_uses_division_not_reciprocal():
+    """Rows built so that fl32(w / s) and fl32(w * fl32(1/s)) round to different integers: only a
+    true float division reproduces the scheme.  The long-double implementation agrees everywhere."""
+    pos = oracle.f16_to_f32(np.arange(1, 0x7C00, dtype=np.uint16))       # every positive finite fp16
+    rows = []
+    for a in oracle.fp16_view(np.geomspace(0.001, 50, 400).astype(np.float32)):
+        s = np.float32(a) / np.float32(127)
+        w = pos[pos < a]
+        div = np.rint(w / s)
+        rec = np.rint(w * (np.float32(1) / s))
+        for v in w[div != rec][:4]:
+            rows.append([a, v] + [0.0] * 6)
+    assert len(rows) >= 8
+    m = np.array(rows, np.float32)
+    q, s, _ = oracle.quantize_rows(m)
+    expect = np.rint(m / s[:, None]).astype(np.int8)
+    assert np.array_equal(q, expect)
+    assert not np.array_equal(q[:, 1], np.rint(m[:, 1] * (np.float32(1) / s)).astype(np.int8))
+    q_ld, s_ld, _ = oracle.quantize_rows(m, longdouble=True)
+    assert np.array_equal(q, q_ld) and np.array_equal(s, s_ld)
+    rng = np.random.default_rng(8)
+    w = oracle.fp16_view(rng.standard_normal((2000, 64), dtype=np.float32) * np.float32(0.02))
+    q, s, _ = oracle.quantize_rows(w)
+    q_ld, s_ld, _ = oracle.quantize_rows(w, longdouble=True)
+    assert np.array_equal(q, q_ld) and np.array_equal(s, s_ld)
+
+
+def test_quantize_fp16_view_and_dequant():
+    rng = np.random.default_rng(9)
+    w32 = rng.standard_normal((64, 768), dtype=np.float32) * np.float32(0.02)
+    q, s, _ = oracle.quantize_fp16_view(w32)
+    q2, s2, _ = oracle.quantize_rows(oracle.fp16_view(w32))
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
+    deq = oracle.dequantize(q, s)
+    assert np.array_equal(deq, (q.astype(np.float32) * s[:, None]).astype(np.float32))
+    assert np.abs(deq - oracle.fp16_view(w32)).max() <= s.max() / 2 * 1.0001   # half a step at most
