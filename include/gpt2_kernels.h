@@ -128,7 +128,7 @@ typedef struct {
 
 /* Backends by the reference's names (cuda/kernels.cuh:88-92).  Here every one of them is built on
  * the MI355X kernels; they differ in which slots are filled, exactly as in the reference:
- *   naive  : one-thread-per-output matmul, simple attention; no matmul_q / gemv / gemv_q
+ *   naive  : one-thread-per-output matmul; no matmul_q / gemv / gemv_q
  *   tiled  : naive + the MFMA GEMM in .matmul
  *   flash  : tiled + the prefill attention kernel in .attention
  *   int8   : flash + .matmul_q (INT8 MFMA GEMM) + .gemv (fp16) + .gemv_q (INT8)
