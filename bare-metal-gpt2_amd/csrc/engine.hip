@@ -18,6 +18,10 @@ void kv_append(uint16_t *K, uint16_t *V, const uint16_t *qkv, StepArg st, int ma
 void attn_decode(uint16_t *att, const uint16_t *qkv, const uint16_t *K, const uint16_t *V, int maxT, StepArg st,
                  int len_imm);
 void argmax_advance(const uint16_t *logits, int V, int *state, int *tokens, int max_pos);
+void attn_decode_append(uint16_t *att, const uint16_t *qkv, uint16_t *K, uint16_t *V, int maxT, StepArg st);
+bool gemv_fused(uint16_t *C, const uint16_t *x, const void *W, const float *Ws, const uint16_t *bias, int N, int K,
+                bool qw, const uint16_t *ln_g, const uint16_t *ln_b, int epi, const uint16_t *resid);
+enum { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2 };
 }  // namespace g2
 
 using namespace g2;
@@ -269,32 +273,70 @@ extern "C" double gpt2_kv_step_bytes(const GPT2KVCache *kv, int len) {
 // ============================================================================ decode step
 // One token (cuda/kvcache.cu:233-269).  With st.state set, token/pos come from device memory and
 // the step ends with the greedy argmax that advances that state (the graph-replayed form).
+//
+// When the backend's GEMV slots are this library's GEMVs, the step runs fused: each LayerNorm is
+// computed inside the GEMV that consumes it, gelu and the residual adds run in the GEMV epilogues,
+// and the K/V append runs inside decode attention -- 5 launches per layer instead of 11.  Other
+// backends (no .gemv: the M=1 matmul fallback) run the reference's unfused sequence.
+static bool fused_decode_ok(const GPT2Backend *be) {
+    return be->gemv == gpt2_gemv_fp16 && (be->gemv_q == nullptr || be->gemv_q == gpt2_gemv_int8) &&
+           be->layernorm == gpt2_layernorm && be->add == gpt2_add && be->gelu == gpt2_gelu;
+}
+
+// One weight-matmul site: (LayerNorm(in) ->) GEMV (-> gelu | + residual into C).  Fused when the
+// backend allows and a fused kernel covers the shape, else the unfused sequence through the
+// backend (LayerNorm into s->ln, GEMV into `tmp` when a residual follows, then gelu / add).
+static void gemv_site(const GPT2Backend *be, bool fused, GPT2ScratchGPU *s, gpt2_half *C, const gpt2_half *in,
+                      const gpt2_half *Wh, const GPT2QW *Wq, const gpt2_half *bias, int N, int K,
+                      const gpt2_half *ln_g, const gpt2_half *ln_b, int epi, gpt2_half *tmp) {
+    const bool q = be->gemv_q && Wq && Wq->q;
+    if (fused && gemv_fused(C, in, q ? (const void *)Wq->q : (const void *)Wh, q ? Wq->s : nullptr, bias, N, K, q,
+                            ln_g, ln_b, epi, epi == EPI_RESID ? C : nullptr))
+        return;
+    const gpt2_half *x = in;
+    if (ln_g) {
+        be->layernorm(s->ln, in, ln_g, ln_b, 1, K);
+        x = s->ln;
+    }
+    gpt2_half *out = (epi == EPI_RESID) ? tmp : C;
+    gpt2_gemv_dispatch(be, out, x, Wh, Wq, bias, N, K);
+    if (epi == EPI_GELU) be->gelu(C, (size_t)N);
+    if (epi == EPI_RESID) be->add(C, tmp, (size_t)N);
+}
+
 static void decode_step(const GPT2Backend *be, const GPT2WeightsGPU *w, GPT2KVCache *kv, StepArg st,
                         GPT2ScratchGPU *s, gpt2_half *logits, gpt2_half *caps, int *state, int *tokens) {
     const int E = GPT2_N_EMBD, Q = GPT2_QKV_DIM, F = GPT2_FFN_DIM, V = GPT2_VOCAB;
     const GPT2QWeightsGPU *qw = w->q;
-    const int len_imm = st.state ? 0 : st.pos + 1;
+    const bool fused = fused_decode_ok(be);
     embed_one(s->x, w->wte, w->wpe, st);
     if (caps) capcpy(caps + (size_t)(GPT2_N_LAYER + 1) * E, s->x, E);
     for (int L = 0; L < GPT2_N_LAYER; ++L) {
         const GPT2LayerGPU *ly = &w->layers[L];
         const GPT2QLayerGPU *qy = qw ? &qw->layers[L] : nullptr;
-        be->layernorm(s->ln, s->x, ly->ln1_g, ly->ln1_b, 1, E);
-        gpt2_gemv_dispatch(be, s->qkv, s->ln, ly->qkv_w, qy ? &qy->qkv_w : nullptr, ly->qkv_b, Q, E);
-        kv_append(gpt2_kv_K(kv, L), gpt2_kv_V(kv, L), s->qkv, st, kv->maxT);
-        attn_decode(s->att, s->qkv, gpt2_kv_K(kv, L), gpt2_kv_V(kv, L), kv->maxT, st, len_imm);
-        gpt2_gemv_dispatch(be, s->ao, s->att, ly->attn_proj_w, qy ? &qy->attn_proj_w : nullptr, ly->attn_proj_b, E, E);
-        be->add(s->x, s->ao, (size_t)E);
-        be->layernorm(s->ln, s->x, ly->ln2_g, ly->ln2_b, 1, E);
-        gpt2_gemv_dispatch(be, s->fc, s->ln, ly->fc_w, qy ? &qy->fc_w : nullptr, ly->fc_b, F, E);
-        be->gelu(s->fc, (size_t)F);
-        gpt2_gemv_dispatch(be, s->ff, s->fc, ly->proj_w, qy ? &qy->proj_w : nullptr, ly->proj_b, E, F);
-        be->add(s->x, s->ff, (size_t)E);
+        gemv_site(be, fused, s, s->qkv, s->x, ly->qkv_w, qy ? &qy->qkv_w : nullptr, ly->qkv_b, Q, E, ly->ln1_g,
+                  ly->ln1_b, EPI_NONE, nullptr);
+        if (fused) {
+            attn_decode_append(s->att, s->qkv, gpt2_kv_K(kv, L), gpt2_kv_V(kv, L), kv->maxT, st);
+        } else {
+            kv_append(gpt2_kv_K(kv, L), gpt2_kv_V(kv, L), s->qkv, st, kv->maxT);
+            attn_decode(s->att, s->qkv, gpt2_kv_K(kv, L), gpt2_kv_V(kv, L), kv->maxT, st, st.state ? 0 : st.pos + 1);
+        }
+        gemv_site(be, fused, s, s->x, s->att, ly->attn_proj_w, qy ? &qy->attn_proj_w : nullptr, ly->attn_proj_b, E, E,
+                  nullptr, nullptr, EPI_RESID, s->ao);
+        gemv_site(be, fused, s, s->fc, s->x, ly->fc_w, qy ? &qy->fc_w : nullptr, ly->fc_b, F, E, ly->ln2_g, ly->ln2_b,
+                  EPI_GELU, nullptr);
+        gemv_site(be, fused, s, s->x, s->fc, ly->proj_w, qy ? &qy->proj_w : nullptr, ly->proj_b, E, F, nullptr, nullptr,
+                  EPI_RESID, s->ff);
         if (caps) capcpy(caps + (size_t)L * E, s->x, E);
     }
-    be->layernorm(s->ln, s->x, w->lnf_g, w->lnf_b, 1, E);
-    if (caps) capcpy(caps + (size_t)GPT2_N_LAYER * E, s->ln, E);
-    if (logits) gpt2_gemv_dispatch(be, logits, s->ln, w->wte, qw ? &qw->wte : nullptr, nullptr, V, E);
+    if (caps) {
+        be->layernorm(s->ln, s->x, w->lnf_g, w->lnf_b, 1, E);
+        capcpy(caps + (size_t)GPT2_N_LAYER * E, s->ln, E);
+    }
+    if (logits)
+        gemv_site(be, fused, s, logits, s->x, w->wte, qw ? &qw->wte : nullptr, nullptr, V, E, w->lnf_g, w->lnf_b,
+                  EPI_NONE, nullptr);
     if (state) argmax_advance(logits, V, state, tokens, kv->maxT);
 }
 

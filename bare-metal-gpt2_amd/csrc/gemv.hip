@@ -63,28 +63,43 @@ __device__ __forceinline__ float slot_sum(float v) {
     return v;
 }
 
+// Epilogues a decode step fuses into its GEMVs.
+enum { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2 };
+
+__device__ __forceinline__ float gelu_tanh(float v) {
+    const float z = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+    return 0.5f * v * (1.0f + tanhf(z));
+}
+
 // LPR lanes per row, CPL 16-byte chunks per lane (row = LPR*CPL chunks), U rows per slot in flight.
-template <int LPR, int CPL, int U, bool QW>
-__global__ __launch_bounds__(256) void k_gemv(uint16_t *__restrict__ C, const uint16_t *__restrict__ x,
+// LN: x is the residual stream and the kernel applies LayerNorm(x; ln_g, ln_b) to it first.  The
+//     LPR lanes of a row slot hold all K values of x between them, so the statistics need no extra
+//     loads: each lane sums its values and the slot reduces (mean, then the biased variance of
+//     x - mean, eps inside the sqrt -- the same formula as k_layernorm); the normalized value is
+//     rounded to fp16, as the standalone LayerNorm's output would be.
+// EPI: EPI_GELU applies gelu_new to (acc*s + bias); EPI_RESID writes resid[n] + (acc*s + bias)
+//     (resid may alias C: each output is read and written by the same lane).
+template <int LPR, int CPL, int U, bool QW, bool LN = false, int EPI = EPI_NONE>
+__global__ __launch_bounds__(256) void k_gemv(uint16_t *C, const uint16_t *__restrict__ x,
                                               const void *__restrict__ Wv, const float *__restrict__ Ws,
-                                              const uint16_t *__restrict__ bias, int N) {
+                                              const uint16_t *__restrict__ bias, int N,
+                                              const uint16_t *__restrict__ ln_g, const uint16_t *__restrict__ ln_b,
+                                              const uint16_t *resid) {
     constexpr int RPW = 64 / LPR;                  // row slots per wave
     constexpr int ROWB = LPR * CPL * 16;           // bytes per weight row
+    constexpr int XV = QW ? 2 * CPL : CPL;         // f16x8 x vectors per lane
     const int lane = threadIdx.x & 63, j = lane % LPR, slot = lane / LPR;
     const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int rbase = wave * (RPW * U) + slot;
 
-    f16x8 xr[QW ? 2 * CPL : CPL];
+    // element offset of x vector v of this lane
+    auto xoff = [&](int v) {
+        if constexpr (QW) return (j + LPR * (v >> 1)) * 16 + (v & 1) * 8;
+        else return (j + LPR * v) * 8;
+    };
+    f16x8 xr[XV];
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-        const int c = j + LPR * i;
-        if constexpr (QW) {
-            xr[2 * i] = *reinterpret_cast<const f16x8 *>(x + c * 16);
-            xr[2 * i + 1] = *reinterpret_cast<const f16x8 *>(x + c * 16 + 8);
-        } else {
-            xr[i] = *reinterpret_cast<const f16x8 *>(x + c * 8);
-        }
-    }
+    for (int v = 0; v < XV; ++v) xr[v] = *reinterpret_cast<const f16x8 *>(x + xoff(v));
 
     const char *W = reinterpret_cast<const char *>(Wv);
     i32x4 wv[U][CPL];
@@ -96,6 +111,33 @@ __global__ __launch_bounds__(256) void k_gemv(uint16_t *__restrict__ C, const ui
             wv[u][i] = (r < N) ? *reinterpret_cast<const i32x4 *>(W + (size_t)r * ROWB + (j + LPR * i) * 16)
                                : i32x4{0, 0, 0, 0};
     }
+
+    if constexpr (LN) {
+        constexpr float invK = 1.0f / (float)(XV * 8 * LPR);
+        float sum = 0.f;
+#pragma unroll
+        for (int v = 0; v < XV; ++v)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sum += (float)xr[v][e];
+        const float mean = slot_sum<LPR>(sum) * invK;
+        float sq = 0.f;
+#pragma unroll
+        for (int v = 0; v < XV; ++v)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float d = (float)xr[v][e] - mean;
+                sq += d * d;
+            }
+        const float rstd = 1.0f / sqrtf(slot_sum<LPR>(sq) * invK + GPT2_LN_EPS);
+#pragma unroll
+        for (int v = 0; v < XV; ++v) {
+            const f16x8 g = *reinterpret_cast<const f16x8 *>(ln_g + xoff(v));
+            const f16x8 b = *reinterpret_cast<const f16x8 *>(ln_b + xoff(v));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xr[v][e] = (f16)(((float)xr[v][e] - mean) * rstd * (float)g[e] + (float)b[e]);
+        }
+    }
+
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int r = rbase + u * RPW;
@@ -110,6 +152,8 @@ __global__ __launch_bounds__(256) void k_gemv(uint16_t *__restrict__ C, const ui
             float v = acc;
             if constexpr (QW) v *= Ws[r];
             if (bias) v += h2f(bias[r]);
+            if constexpr (EPI == EPI_GELU) v = gelu_tanh(v);
+            if constexpr (EPI == EPI_RESID) v += h2f(resid[r]);
             C[r] = f2h(v);
         }
     }
@@ -139,7 +183,8 @@ __global__ __launch_bounds__(256) void k_gemv_generic(uint16_t *__restrict__ C, 
     }
 }
 
-typedef void (*GemvFn)(uint16_t *, const uint16_t *, const void *, const float *, const uint16_t *, int);
+typedef void (*GemvFn)(uint16_t *, const uint16_t *, const void *, const float *, const uint16_t *, int,
+                       const uint16_t *, const uint16_t *, const uint16_t *);
 
 struct GemvCfg {
     int row_chunks;   // 16-byte chunks per row this kernel is built for
@@ -201,7 +246,8 @@ void gemv(uint16_t *C, const uint16_t *x, const void *W, const float *Ws, const 
         const GemvCfg &g = kGv[c];
         const int waves = cdiv(N, g.rows_per_wave);
         const int blocks = cdiv(waves, g.waves_per_block);
-        hipLaunchKernelGGL(g.fn, dim3(blocks), dim3(64 * g.waves_per_block), 0, stream(), C, x, W, Ws, bias, N);
+        hipLaunchKernelGGL(g.fn, dim3(blocks), dim3(64 * g.waves_per_block), 0, stream(), C, x, W, Ws, bias, N,
+                           nullptr, nullptr, nullptr);
         check_launch(qw ? "k_gemv<int8>" : "k_gemv<fp16>");
         return;
     }
@@ -209,6 +255,41 @@ void gemv(uint16_t *C, const uint16_t *x, const void *W, const float *Ws, const 
     if (qw) hipLaunchKernelGGL(k_gemv_generic<true>, dim3(blocks), dim3(256), 0, stream(), C, x, W, Ws, bias, N, K);
     else hipLaunchKernelGGL(k_gemv_generic<false>, dim3(blocks), dim3(256), 0, stream(), C, x, W, Ws, bias, N, K);
     check_launch("k_gemv_generic");
+}
+
+// Fused decode GEMVs: (LayerNorm ->) GEMV (-> gelu | + residual).  Returns false when no fused
+// kernel covers the shape (the caller then runs the unfused sequence).
+struct FusedGemv {
+    int row_chunks;
+    bool qw, ln;
+    int epi;
+    int rows_per_wave;
+    GemvFn fn;
+};
+
+#define G2_FG(LPR, CPL, QW, LN, EPI) {LPR * CPL, QW, LN, EPI, 64 / LPR, k_gemv<LPR, CPL, 1, QW, LN, EPI>}
+static const FusedGemv kFused[] = {
+    G2_FG(16, 3, true, true, EPI_NONE),  G2_FG(16, 3, true, true, EPI_GELU),   G2_FG(16, 3, true, false, EPI_RESID),
+    G2_FG(16, 12, true, false, EPI_RESID),
+    G2_FG(16, 6, false, true, EPI_NONE), G2_FG(16, 6, false, true, EPI_GELU),  G2_FG(16, 6, false, false, EPI_RESID),
+    G2_FG(64, 6, false, false, EPI_RESID),
+};
+
+bool gemv_fused(uint16_t *C, const uint16_t *x, const void *W, const float *Ws, const uint16_t *bias, int N, int K,
+                bool qw, const uint16_t *ln_g, const uint16_t *ln_b, int epi, const uint16_t *resid) {
+    const bool ln = ln_g != nullptr;
+    const long row_bytes = qw ? (long)K : 2L * K;
+    if (N <= 0 || K <= 0 || row_bytes % 16 || !aligned16(W) || !aligned16(x)) return false;
+    if (ln && (!aligned16(ln_g) || !aligned16(ln_b))) return false;
+    const int rc = (int)(row_bytes / 16);
+    for (const FusedGemv &f : kFused) {
+        if (f.row_chunks != rc || f.qw != qw || f.ln != ln || f.epi != epi) continue;
+        const int blocks = cdiv(cdiv(N, f.rows_per_wave), 4);
+        hipLaunchKernelGGL(f.fn, dim3(blocks), dim3(256), 0, stream(), C, x, W, Ws, bias, N, ln_g, ln_b, resid);
+        check_launch("k_gemv<fused>");
+        return true;
+    }
+    return false;
 }
 
 }  // namespace g2

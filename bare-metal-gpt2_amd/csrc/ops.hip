@@ -131,23 +131,28 @@ __global__ void k_add8(f16x8 *__restrict__ x, const f16x8 *__restrict__ y, size_
 
 // ------------------------------------------------------------------ attention
 // One wave attends one query (64 dims) over keys [j0, j1) of one head.  Keys are rows
-// `kbase + j*stride`, values `vbase + j*stride` (halves).  Lane = key inside a 64-key chunk for the
-// scores; for the context, lanes 0-31 take even keys and lanes 32-63 odd keys, two dims per lane.
-// Running state: max m, exp-sum l, context (c0, c1) for dims 2*(lane&31) and +1.
+// `kbase + j*stride`, values `vbase + j*stride` (halves).  Scores: lane = key inside a 64-key chunk,
+// each lane reading its own 128-byte key row (64 consecutive rows = contiguous bytes in the cache).
+// Context: lane = (key slot l>>3, dim group l&7): eight lanes read one 128-byte value row with
+// 16-byte loads, so one load instruction covers 8 keys; every lane accumulates 8 dims over its key
+// slot, and the 8 slots are summed once at the end.  Online softmax across chunks (m, l, c[8]).
+// Row jcur (if any) is read from kcur / vcur instead of the strided rows: the decode step's own key
+// and value, taken straight from its qkv row while the cache copy is being written.
 struct AttnState {
-    float m, l, c0, c1;
+    float m, l, c[8];
 };
 
 __device__ __forceinline__ void attend_range(const f16x8 (&q)[8], const uint16_t *__restrict__ kbase,
                                              const uint16_t *__restrict__ vbase, long stride, int j0, int j1,
-                                             float scale, AttnState &st) {
+                                             float scale, AttnState &st, int jcur = -1,
+                                             const uint16_t *kcur = nullptr, const uint16_t *vcur = nullptr) {
     const int lane = threadIdx.x & 63;
-    const int half = lane >> 5, d2 = 2 * (lane & 31);
+    const int slot = lane >> 3, dg = (lane & 7) * 8;
     for (int jc = j0; jc < j1; jc += 64) {
         const int j = jc + lane;
         float s = -INFINITY;
         if (j < j1) {
-            const uint16_t *kr = kbase + (size_t)j * stride;
+            const uint16_t *kr = (j == jcur) ? kcur : kbase + (size_t)j * stride;
             float dot = 0.f;
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
@@ -163,25 +168,44 @@ __device__ __forceinline__ void attend_range(const f16x8 (&q)[8], const uint16_t
         const float p = (j < j1) ? __expf(s - mnew) : 0.f;
         const float corr = __expf(st.m - mnew);         // st.m = -inf on the first chunk -> 0
         st.l = st.l * corr + wave_sum(p);
-        st.c0 *= corr;
-        st.c1 *= corr;
         st.m = mnew;
-        const int nkeys = min(64, j1 - jc);
-        for (int jj = 0; jj < nkeys; jj += 2) {
-            const int key = jj + half;
-            const float pj = __shfl(p, key, 64);
-            if (key < nkeys) {
-                const f16x2 vv = *reinterpret_cast<const f16x2 *>(vbase + (size_t)(jc + key) * stride + d2);
-                st.c0 += pj * (float)vv[0];
-                st.c1 += pj * (float)vv[1];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) st.c[e] *= corr;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int kidx = slot + 8 * t;              // key index inside the chunk
+            const float pj = __shfl(p, kidx, 64);
+            const int key = jc + kidx;
+            if (key < j1) {
+                const uint16_t *vr = (key == jcur) ? vcur : vbase + (size_t)key * stride;
+                const f16x8 vv = *reinterpret_cast<const f16x8 *>(vr + dg);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) st.c[e] += pj * (float)vv[e];
             }
         }
+    }
+}
+
+// Sum the context over the 8 key slots; lanes 0..7 then hold dims 8*lane .. 8*lane+7.
+__device__ __forceinline__ void reduce_slots(AttnState &st) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        st.c[e] += __shfl_xor(st.c[e], 8, 64);
+        st.c[e] += __shfl_xor(st.c[e], 16, 64);
+        st.c[e] += __shfl_xor(st.c[e], 32, 64);
     }
 }
 
 __device__ __forceinline__ void load_q(f16x8 (&q)[8], const uint16_t *qp) {
 #pragma unroll
     for (int c = 0; c < 8; ++c) q[c] = *reinterpret_cast<const f16x8 *>(qp + 8 * c);
+}
+
+__device__ __forceinline__ void init_state(AttnState &st) {
+    st.m = -INFINITY;
+    st.l = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) st.c[e] = 0.f;
 }
 
 // Prefill: grid (ceil(T/4), H), four waves = four consecutive queries of one head.
@@ -193,43 +217,31 @@ __global__ __launch_bounds__(256) void k_attention_prefill(uint16_t *__restrict_
     if (i >= T) return;
     f16x8 q[8];
     load_q(q, qkv + (size_t)i * S + h * D);
-    AttnState st = {-INFINITY, 0.f, 0.f, 0.f};
+    AttnState st;
+    init_state(st);
     attend_range(q, qkv + E + h * D, qkv + 2 * E + h * D, S, 0, i + 1, 0.125f, st);
-    st.c0 += __shfl_xor(st.c0, 32, 64);
-    st.c1 += __shfl_xor(st.c1, 32, 64);
-    if (lane < 32) {
+    reduce_slots(st);
+    if (lane < 8) {
         const float inv = 1.0f / st.l;
-        f16x2 r = {(f16)(st.c0 * inv), (f16)(st.c1 * inv)};
-        *reinterpret_cast<f16x2 *>(att + (size_t)i * E + h * D + 2 * lane) = r;
+        f16x8 r;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[e] = (f16)(st.c[e] * inv);
+        *reinterpret_cast<f16x8 *>(att + (size_t)i * E + h * D + 8 * lane) = r;
     }
 }
 
-// Decode: one work-group per head, NW waves split the keys [0, len); partial (m, l, c) states are
-// merged through LDS.  len = pos + 1 comes from the step argument.
+// Merge the NW waves' partial (m, l, c) states of one head through LDS and write the context.
 template <int NW>
-__global__ __launch_bounds__(64 * NW) void k_attn_decode(uint16_t *__restrict__ att, const uint16_t *__restrict__ qkv,
-                                                         const uint16_t *__restrict__ Kc, const uint16_t *__restrict__ Vc,
-                                                         int maxT, StepArg st_arg, int len_imm) {
-    constexpr int D = GPT2_HEAD_DIM;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, h = blockIdx.x;
-    const int len = min(len_imm > 0 ? len_imm : st_arg.p() + 1, maxT);
-    const int per = ((len + NW - 1) / NW + 63) & ~63;
-    const int j0 = min(len, w * per), j1 = min(len, j0 + per);
-    f16x8 q[8];
-    load_q(q, qkv + h * D);
-    AttnState st = {-INFINITY, 0.f, 0.f, 0.f};
-    const uint16_t *kb = Kc + (size_t)h * maxT * D, *vb = Vc + (size_t)h * maxT * D;
-    if (j0 < j1) attend_range(q, kb, vb, D, j0, j1, 0.125f, st);
-    st.c0 += __shfl_xor(st.c0, 32, 64);
-    st.c1 += __shfl_xor(st.c1, 32, 64);
-    __shared__ float sm[NW], sl[NW], sc[NW][D];
+__device__ __forceinline__ void merge_waves(const AttnState &st, uint16_t *__restrict__ out) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    __shared__ float sm[NW], sl[NW], sc[NW][GPT2_HEAD_DIM];
     if (lane == 0) {
         sm[w] = st.m;
         sl[w] = st.l;
     }
-    if (lane < 32) {
-        sc[w][2 * lane] = st.c0;
-        sc[w][2 * lane + 1] = st.c1;
+    if (lane < 8) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sc[w][8 * lane + e] = st.c[e];
     }
     __syncthreads();
     if (w == 0) {
@@ -242,8 +254,57 @@ __global__ __launch_bounds__(64 * NW) void k_attn_decode(uint16_t *__restrict__ 
             L += sl[i] * f;
             c += sc[i][lane] * f;
         }
-        att[h * D + lane] = f2h(c / L);
+        out[lane] = f2h(c / L);
     }
+}
+
+// Decode: one work-group per head, NW waves split the keys [0, len); partial (m, l, c) states are
+// merged through LDS.  len = pos + 1 comes from the step argument.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void k_attn_decode(uint16_t *__restrict__ att, const uint16_t *__restrict__ qkv,
+                                                         const uint16_t *__restrict__ Kc, const uint16_t *__restrict__ Vc,
+                                                         int maxT, StepArg st_arg, int len_imm) {
+    constexpr int D = GPT2_HEAD_DIM;
+    const int w = threadIdx.x >> 6, h = blockIdx.x;
+    const int len = min(len_imm > 0 ? len_imm : st_arg.p() + 1, maxT);
+    const int per = ((len + NW - 1) / NW + 7) & ~7;   // keys per wave (multiple of 8)
+    const int j0 = min(len, w * per), j1 = min(len, j0 + per);
+    f16x8 q[8];
+    load_q(q, qkv + h * D);
+    AttnState st;
+    init_state(st);
+    const uint16_t *kb = Kc + (size_t)h * maxT * D, *vb = Vc + (size_t)h * maxT * D;
+    if (j0 < j1) attend_range(q, kb, vb, D, j0, j1, 0.125f, st);
+    reduce_slots(st);
+    merge_waves<NW>(st, att + h * D);
+}
+
+// Decode step, fused: appends this position's K and V (head h's 64 values of each) to the cache and
+// attends over [0, pos], reading key/value pos from the qkv row itself.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void k_attn_decode_append(uint16_t *__restrict__ att, const uint16_t *__restrict__ qkv,
+                                                                uint16_t *__restrict__ Kc, uint16_t *__restrict__ Vc,
+                                                                int maxT, StepArg st_arg) {
+    constexpr int E = GPT2_N_EMBD, D = GPT2_HEAD_DIM;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, h = blockIdx.x;
+    const int pos = st_arg.p();
+    if ((unsigned)pos >= (unsigned)maxT) return;   // uniform over the grid: nothing to attend
+    const size_t hoff = (size_t)h * maxT * D;
+    if (w == 0) {
+        Kc[hoff + (size_t)pos * D + lane] = qkv[E + h * D + lane];
+        Vc[hoff + (size_t)pos * D + lane] = qkv[2 * E + h * D + lane];
+    }
+    const int len = pos + 1;
+    const int per = ((len + NW - 1) / NW + 7) & ~7;   // keys per wave (multiple of 8)
+    const int j0 = min(len, w * per), j1 = min(len, j0 + per);
+    f16x8 q[8];
+    load_q(q, qkv + h * D);
+    AttnState st;
+    init_state(st);
+    if (j0 < j1)
+        attend_range(q, Kc + hoff, Vc + hoff, D, j0, j1, 0.125f, st, pos, qkv + E + h * D, qkv + 2 * E + h * D);
+    reduce_slots(st);
+    merge_waves<NW>(st, att + h * D);
 }
 
 // ------------------------------------------------------------------ KV cache writes
@@ -344,8 +405,13 @@ void kv_append(uint16_t *K, uint16_t *V, const uint16_t *qkv, StepArg st, int ma
 
 void attn_decode(uint16_t *att, const uint16_t *qkv, const uint16_t *K, const uint16_t *V, int maxT, StepArg st,
                  int len_imm) {
-    hipLaunchKernelGGL(k_attn_decode<8>, dim3(GPT2_N_HEAD), dim3(512), 0, stream(), att, qkv, K, V, maxT, st, len_imm);
+    hipLaunchKernelGGL(k_attn_decode<16>, dim3(GPT2_N_HEAD), dim3(1024), 0, stream(), att, qkv, K, V, maxT, st, len_imm);
     check_launch("k_attn_decode");
+}
+
+void attn_decode_append(uint16_t *att, const uint16_t *qkv, uint16_t *K, uint16_t *V, int maxT, StepArg st) {
+    hipLaunchKernelGGL(k_attn_decode_append<16>, dim3(GPT2_N_HEAD), dim3(1024), 0, stream(), att, qkv, K, V, maxT, st);
+    check_launch("k_attn_decode_append");
 }
 
 void argmax_advance(const uint16_t *logits, int V, int *state, int *tokens, int max_pos) {
