@@ -5,19 +5,21 @@
 //   * v_mfma_f32_16x16x32_f16: W rows feed the MFMA "A" operand and activation rows the "B"
 //     operand, so the accumulator holds D[n][m] = C[m][n] and each lane owns four consecutive n of
 //     one output row m: the epilogue writes 8-byte vectors into row-major C.
-//   * Both operands are K-contiguous, so a 16-byte global load is 8 consecutive k of one row.  Tiles
-//     are staged through LDS, double-buffered (one barrier per k-tile), with the 16-byte chunk index
-//     XOR-swizzled by row so that the ds_read_b128 fragment reads and the ds_write_b128 stores hit
-//     distinct banks.
-//   * The MFMA k-lane mapping only has to agree between the two operands (a dot product is order
-//     free), so each lane group reads 8 consecutive k of its row for both A and B.
-//   * INT8 weights (weight-only scheme) are converted to fp16 while staging: |q| <= 127 is exact in
-//     fp16 and the int8 x fp16 products are exact in fp32, so the MFMA path is the fp16 one; the
-//     per-row scale is applied once in the epilogue, then the bias (cuda/kernels_quant.cu:56-59).
+//   * Both operands are K-contiguous, so a 16-byte load is 8 consecutive k of one row.  The MFMA
+//     k-lane mapping only has to agree between the two operands (a dot product is order free), so
+//     each lane group reads 8 consecutive k of its row for both.
+//   * Main path k_gemm_dl: tiles go global -> LDS with global_load_lds_dwordx4 through an S-stage
+//     ring (no VGPR staging), the 16-byte chunk index XOR-swizzled by row so fragment reads hit
+//     distinct banks; one barrier per 64-wide k-tile.
+//   * INT8 weights (weight-only scheme) stay int8 in LDS and are widened to exact fp16 as fragments
+//     are read: |q| <= 127 is exact in fp16 and int8 x fp16 products are exact in fp32, so the
+//     MFMA path is the fp16 one; the per-row scale is applied once in the epilogue, then the bias
+//     (cuda/kernels_quant.cu:56-59).
 //   * Work-group -> tile mapping is XCD-aware: consecutive work-groups go round robin over the 8
 //     XCDs, so each XCD is given one contiguous run of tiles (n-major, m fastest), and the W tiles it
 //     reads stay in its own L2.
-// Shapes or pointers the MFMA path cannot take (K % 8 != 0, or unaligned rows) run k_gemm_generic.
+//   * k_gemm_mfma (register-ring pipeline) takes K % 64 != 0 shapes in its predicated form; shapes
+//     or pointers no MFMA path can take (K % 8 != 0, unaligned rows) run k_gemm_generic.
 #include <cstdlib>
 #include <cstring>
 
@@ -249,6 +251,226 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(uint16_t *__restrict__ C, con
     }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Direct-to-LDS pipeline (k_gemm_dl).  The per-CU data paths measured on MI355X set the design:
+// global (L1/L2 hit) -> CU 64 B/clk, LDS reads 126 B/clk with 4 waves per CU and 234 B/clk with 8,
+// fp16 MFMA 4096 FLOP/clk.  So:
+//   * tiles are fetched with global_load_lds_dwordx4: each wave instruction moves 1 KB straight
+//     into LDS, with no VGPR staging, no ds_write and no register ring;
+//   * S LDS stages are in flight (S-1 k-tiles of loads outstanding while one is consumed), and the
+//     pipeline drains exactly: no k-tile is fetched twice;
+//   * the 16-byte chunk swizzle of the LDS rows is made by choosing which global chunk each lane
+//     fetches (lane i of an instruction always lands at byte 16*i of its 1 KB);
+//   * INT8 weights stay int8 in LDS (half the bytes) and are widened to exact fp16 as fragments
+//     are read;
+//   * one barrier per k-tile: the buffer refilled at step kt was last read at step kt-1.
+// s_waitcnt immediate for "at most n vector-memory operations outstanding" (gfx9 encoding, expcnt
+// and lgkmcnt left unconstrained).
+template <int n>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
+}
+
+// Wait until at most `after` k-tiles of this wave's loads (L instructions each) are outstanding.
+template <int L, int MAXA>
+__device__ __forceinline__ void wait_tiles(int after) {
+    if constexpr (MAXA >= 0) {
+        if (after == MAXA) { wait_vm<L * MAXA>(); return; }
+        wait_tiles<L, MAXA - 1>(after);
+    }
+}
+
+__device__ __forceinline__ f16x8 i8x8_to_f16x8(uint2 w) {
+    uint32_t h[4];
+    i8x4_to_f16x4(w.x, h[0], h[1]);
+    i8x4_to_f16x4(w.y, h[2], h[3]);
+    const i32x4 v = {(int)h[0], (int)h[1], (int)h[2], (int)h[3]};
+    return __builtin_bit_cast(f16x8, v);
+}
+
+#define G2_LDS(p) ((__attribute__((address_space(3))) void *)(p))
+
+// Work-group barrier for the LDS ring: the caller has already waited (vmcnt) for its own loads of
+// the tile about to be read; the LDS reads of the previous tile completed before their MFMAs.  The
+// "memory" clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int BN, int BM, int WN, int WM, int S, bool QW>
+__global__ __launch_bounds__(WN *WM * 64) void k_gemm_dl(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
+                                                         const void *__restrict__ Wv, const float *__restrict__ Ws,
+                                                         const uint16_t *__restrict__ bias, int M, int N, int K,
+                                                         int tiles_m, int ntiles, int vec_store) {
+#if defined(__HIP_DEVICE_COMPILE__)   // LDS address-space pointers exist only in the device pass
+    constexpr int NW = WN * WM;
+    constexpr int BK = 64;
+    constexpr int A_BYTES = BM * BK * 2;        // fp16 A tile: rows of 128 B (8 chunks)
+    constexpr int W_ROWB = QW ? BK : BK * 2;    // W tile rows: 64 B int8 (4 chunks) or 128 B fp16
+    constexpr int W_BYTES = BN * W_ROWB;
+    constexpr int STAGE = A_BYTES + W_BYTES;
+    constexpr int A_INS = A_BYTES / 1024, W_INS = W_BYTES / 1024;
+    static_assert(A_BYTES % 1024 == 0 && W_BYTES % 1024 == 0, "1 KB load granules");
+    constexpr int TOT = A_INS + W_INS, LO = TOT / NW, REM = TOT % NW, LMAX = LO + (REM ? 1 : 0);
+    constexpr int WTN = BN / WN, WTM = BM / WM, TN = WTN / 16, TM = WTM / 16;
+    static_assert(TN * 16 == WTN && TM * 16 == WTM, "wave tile is whole 16x16 blocks");
+    static_assert(S >= 2 && (S - 2) * LMAX < 64, "stages");
+
+    __shared__ __attribute__((aligned(1024))) char smem[S * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nk = K / BK;
+    const size_t welt = QW ? 1 : 2;
+    const int tile = xcd_tile(blockIdx.x, ntiles);
+    const int n0 = (tile / tiles_m) * BN, m0 = (tile % tiles_m) * BM;
+    const int wn0 = (wave / WM) * WTN, wm0 = (wave % WM) * WTM;
+
+    // This wave's load instructions: global source (at k = 0) and LDS offset inside a stage.
+    const char *gsrc[LMAX];
+    int ldst[LMAX], kstep[LMAX];
+#pragma unroll
+    for (int j = 0; j < LMAX; ++j) {
+        const int q = wave + NW * j;
+        if (q < A_INS) {
+            const int row = 8 * q + (lane >> 3), c = (lane & 7) ^ (row & 7);
+            const int m = min(m0 + row, M - 1);
+            gsrc[j] = reinterpret_cast<const char *>(A + (size_t)m * K + c * 8);
+            ldst[j] = q * 1024;
+            kstep[j] = BK * 2;
+        } else {
+            const int qw = min(q, TOT - 1) - A_INS;
+            int row, c;
+            if constexpr (QW) { row = 16 * qw + (lane >> 2); c = (lane & 3) ^ ((row >> 2) & 3); }
+            else { row = 8 * qw + (lane >> 3); c = (lane & 7) ^ (row & 7); }
+            const int n = min(n0 + row, N - 1);
+            gsrc[j] = reinterpret_cast<const char *>(Wv) + (size_t)n * K * welt + c * 16;
+            ldst[j] = A_BYTES + qw * 1024;
+            kstep[j] = BK * (int)welt;
+        }
+    }
+    const int nld = (REM == 0 || wave < REM) ? LMAX : LO;   // wave-uniform
+    auto issue = [&](int kt) {
+        char *st = smem + (kt % S) * STAGE;
+#pragma unroll
+        for (int j = 0; j < LMAX; ++j)
+            if (j < nld)
+                __builtin_amdgcn_global_load_lds(gsrc[j] + (size_t)kt * kstep[j], G2_LDS(st + ldst[j]), 16, 0, 0);
+    };
+    auto wait_for = [&](int after) {
+        if constexpr (REM == 0) wait_tiles<LO, S - 2>(after);
+        else {
+            if (wave < REM) wait_tiles<LO + 1, S - 2>(after);
+            else wait_tiles<LO, S - 2>(after);
+        }
+    };
+
+    f32x4 acc[TN][TM];
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+        for (int b = 0; b < TM; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int lrow = lane & 15, lgrp = lane >> 4;
+
+    // Fragments of one k-tile (2 MFMA k-steps of 32): A rows as the MFMA B operand, W rows as the
+    // A operand (int8 W kept as raw codes until the MFMA phase).
+    struct Frag {
+        f16x8 fa[2][TM];
+        f16x8 fw[2][TN];
+        uint2 wq[2][TN];
+    };
+    auto load_frags = [&](int kt, Frag &F) {
+        const char *st = smem + (kt % S) * STAGE;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int c = ks * 4 + lgrp;
+#pragma unroll
+            for (int b = 0; b < TM; ++b) {
+                const int r = wm0 + b * 16 + lrow;
+                F.fa[ks][b] = *reinterpret_cast<const f16x8 *>(st + r * 128 + ((c ^ (r & 7)) << 4));
+            }
+#pragma unroll
+            for (int a = 0; a < TN; ++a) {
+                const int r = wn0 + a * 16 + lrow;
+                if constexpr (QW) {
+                    const int cq = (ks * 2 + (lgrp >> 1)) ^ ((r >> 2) & 3);
+                    F.wq[ks][a] = *reinterpret_cast<const uint2 *>(st + A_BYTES + r * 64 + (cq << 4) + ((lgrp & 1) << 3));
+                } else {
+                    F.fw[ks][a] = *reinterpret_cast<const f16x8 *>(st + A_BYTES + r * 128 + ((c ^ (r & 7)) << 4));
+                }
+            }
+        }
+    };
+    auto mfmas = [&](const Frag &F) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int a = 0; a < TN; ++a) {
+                f16x8 w;
+                if constexpr (QW) w = i8x8_to_f16x8(F.wq[ks][a]);
+                else w = F.fw[ks][a];
+#pragma unroll
+                for (int b = 0; b < TM; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, F.fa[ks][b], acc[a][b], 0, 0, 0);
+            }
+    };
+
+    // Prologue: tiles 0 .. S-2 in flight (the config table requires nk >= S - 1).
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s) issue(s);
+    int kt = 0;
+    for (; kt + S - 1 < nk; ++kt) {
+        wait_for(S - 2);
+        lds_barrier();
+        issue(kt + S - 1);
+        Frag F;
+        load_frags(kt, F);
+        mfmas(F);
+    }
+    for (; kt < nk; ++kt) {
+        wait_for(nk - 1 - kt);
+        lds_barrier();
+        Frag F;
+        load_frags(kt, F);
+        mfmas(F);
+    }
+
+    // Epilogue: lane holds D[n][m] for n = nb..nb+3, m = mrow.
+#pragma unroll
+    for (int a = 0; a < TN; ++a) {
+        const int nb = n0 + wn0 + a * 16 + lgrp * 4;
+        float sc[4] = {1.f, 1.f, 1.f, 1.f}, bs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (nb + i < N) {
+                if constexpr (QW) sc[i] = Ws[nb + i];
+                if (bias) bs[i] = h2f(bias[nb + i]);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+            const int m = m0 + wm0 + b * 16 + lrow;
+            if (m >= M) continue;
+            uint16_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float v = acc[a][b][i];
+                if constexpr (QW) v = v * sc[i];
+                o[i] = f2h(v + bs[i]);
+            }
+            uint16_t *dst = C + (size_t)m * N + nb;
+            if (vec_store && nb + 3 < N) {
+                const uint2 pk = {(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+                *reinterpret_cast<uint2 *>(dst) = pk;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (nb + i < N) dst[i] = o[i];
+            }
+        }
+    }
+#endif
+}
+
 // Any shape, any alignment: 16x16 outputs per work-group, k staged through LDS as fp32.
 template <bool QW>
 __global__ __launch_bounds__(256) void k_gemm_generic(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
@@ -294,41 +516,40 @@ __global__ void k_gemm_naive(uint16_t *__restrict__ C, const uint16_t *__restric
 // ---------------------------------------------------------------------------- tile table
 struct GemmCfg {
     int bn, bm, kmul;   // K must be a multiple of kmul (BK * DEPTH, or 8 for the guarded kernel)
+    int kmin, threads;  // and at least kmin; work-group size
     void (*fp16)(uint16_t *, const uint16_t *, const void *, const float *, const uint16_t *, int, int, int, int, int, int);
     void (*int8)(uint16_t *, const uint16_t *, const void *, const float *, const uint16_t *, int, int, int, int, int, int);
     const char *name;
 };
 
 #define G2_CFG(BN, BM, BK, WN, WM, D) \
-    {BN, BM, BK * D, k_gemm_mfma<BN, BM, BK, WN, WM, false, D>, k_gemm_mfma<BN, BM, BK, WN, WM, true, D>, \
+    {BN, BM, BK * D, 0, 256, k_gemm_mfma<BN, BM, BK, WN, WM, false, D>, k_gemm_mfma<BN, BM, BK, WN, WM, true, D>, \
      "bn" #BN "_bm" #BM "_bk" #BK "_w" #WN "x" #WM "_d" #D}
-
+// Direct-to-LDS pipeline: K % 64 == 0 and at least S-1 k-tiles.
+#define G2_DCFG(BN, BM, WN, WM, S) \
+    {BN, BM, 64, 64 * (S - 1), 64 * WN * WM, k_gemm_dl<BN, BM, WN, WM, S, false>, k_gemm_dl<BN, BM, WN, WM, S, true>, \
+     "dl_bn" #BN "_bm" #BM "_w" #WN "x" #WM "_s" #S}
 static const GemmCfg kCfgs[] = {
-    G2_CFG(128, 128, 64, 2, 2, 2),  // 0: wave tile 64x64
-    G2_CFG(128, 64, 64, 2, 2, 4),   // 1: wave tile 64x32
-    G2_CFG(64, 128, 64, 2, 2, 4),   // 2: wave tile 32x64
-    G2_CFG(64, 64, 64, 2, 2, 6),    // 3: wave tile 32x32
-    G2_CFG(128, 32, 64, 4, 1, 6),   // 4: wave tile 32x32
-    G2_CFG(64, 32, 64, 2, 2, 6),    // 5: wave tile 32x16
-    G2_CFG(32, 64, 64, 1, 4, 6),    // 6: wave tile 32x16
-    G2_CFG(96, 64, 64, 2, 2, 6),    // 7: wave tile 48x32
-    G2_CFG(64, 64, 64, 2, 2, 12),   // 8: wave tile 32x32, whole K=768 in flight
-    G2_CFG(64, 32, 64, 2, 2, 12),   // 9: wave tile 32x16
-    G2_CFG(32, 32, 64, 2, 2, 12),   // 10: wave tile 16x16
-    G2_CFG(96, 32, 64, 2, 2, 6),    // 11: wave tile 48x16
-    G2_CFG(64, 64, 64, 2, 2, 1),    // 12: no prefetch ring (reference point)
-    G2_CFG(64, 64, 128, 2, 2, 3),   // 13: BK=128: half the barriers
-    G2_CFG(96, 64, 128, 2, 2, 3),   // 14
-    G2_CFG(64, 32, 128, 2, 2, 3),   // 15
-    G2_CFG(32, 64, 128, 1, 4, 3),   // 16
-    G2_CFG(64, 64, 128, 2, 2, 2),   // 17
-    G2_CFG(128, 64, 128, 2, 2, 2),  // 18
+    G2_DCFG(96, 64, 2, 4, 4),       // 0: 8 waves, wave tile 48x16 (QKV)
+    G2_DCFG(128, 64, 4, 2, 3),      // 1: 8 waves, wave tile 32x32 (fc)
+    G2_DCFG(32, 64, 1, 4, 4),       // 2: 4 waves, wave tile 32x16 (attn-proj, mlp-proj)
+    G2_DCFG(64, 32, 2, 2, 4),       // 3: 4 waves, wave tile 32x16
+    G2_DCFG(96, 64, 2, 2, 6),       // 4: 4 waves, wave tile 48x32
+    G2_DCFG(64, 64, 2, 4, 4),       // 5: 8 waves, wave tile 32x16
+    G2_DCFG(128, 128, 2, 4, 4),     // 6: 8 waves, wave tile 64x32
+    G2_DCFG(256, 128, 4, 2, 3),     // 7: 8 waves, wave tile 64x64
+    G2_DCFG(32, 32, 1, 2, 4),       // 8: 2 waves, wave tile 32x16
+    // register-ring pipeline (k_gemm_mfma), kept as a reference point for tuning
+    G2_CFG(96, 64, 64, 2, 2, 6),    // 9: wave tile 48x32
+    G2_CFG(64, 32, 64, 2, 2, 6),    // 10: wave tile 32x16
+    G2_CFG(32, 64, 64, 1, 4, 6),    // 11: wave tile 32x16
+    G2_CFG(128, 128, 64, 2, 2, 2),  // 12: wave tile 64x64
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
 
 // Any K % 8 == 0 (int8: K % 16 == 0): predicated loads, one k-tile of prefetch.
 #define G2_GCFG(BN, BM, WN, WM) \
-    {BN, BM, 8, k_gemm_mfma<BN, BM, 64, WN, WM, false, 1, true>, k_gemm_mfma<BN, BM, 64, WN, WM, true, 1, true>, \
+    {BN, BM, 8, 0, 256, k_gemm_mfma<BN, BM, 64, WN, WM, false, 1, true>, k_gemm_mfma<BN, BM, 64, WN, WM, true, 1, true>, \
      "guard_bn" #BN "_bm" #BM}
 static const GemmCfg kGuardCfgs[] = {
     G2_GCFG(64, 64, 2, 2),
@@ -337,7 +558,7 @@ static const GemmCfg kGuardCfgs[] = {
 
 static int g_force_cfg = -2;  // -2: not read yet; -1: table
 
-static bool cfg_fits(int c, int K) { return K % kCfgs[c].kmul == 0; }
+static bool cfg_fits(int c, int K) { return K % kCfgs[c].kmul == 0 && K >= kCfgs[c].kmin; }
 
 static int pick_cfg(int M, int N, int K) {
     if (g_force_cfg == -2) {
@@ -346,18 +567,19 @@ static int pick_cfg(int M, int N, int K) {
         if (g_force_cfg >= kNumCfgs) g_force_cfg = -1;
     }
     if (g_force_cfg >= 0 && cfg_fits(g_force_cfg, K)) return g_force_cfg;
-    // Measured picks for the GPT-2 prefill shapes at M in (256, 512] (12-layer sweeps with L2-cold
-    // weights on MI355X), then a fallback: the largest tile that still gives about one work-group
-    // per CU (256 CUs), among the configs whose ring depth divides K; -1 when none does (the
-    // guarded kernel runs).
+    // Measured picks for the GPT-2 prefill shapes at M in (256, 512] (12-layer sweeps with
+    // distinct, L2-cold weights per launch on MI355X), then a fallback: the largest tile that still
+    // gives about one work-group per CU (256 CUs), among the configs whose K constraint holds; -1
+    // when none does (the guarded kernel runs).
     if (M > 256 && M <= 512) {
         int c = -1;
-        if (N == 768 && K == 768) c = 6;          // attn-proj: 32x64, depth 6
-        else if (N == 768 && K == 3072) c = 5;    // mlp-proj: 64x32, depth 6
-        else if (N >= 2048 && K == 768) c = 7;    // QKV, fc: 96x64, depth 6
+        if (N == 768 && K == 768) c = 3;                  // attn-proj: 64x32, 4 waves, 4 stages
+        else if (N == 768 && K == 3072) c = 2;            // mlp-proj: 32x64, 4 waves, 4 stages
+        else if (N == 2304 && K == 768) c = 0;            // QKV: 96x64, 8 waves, 4 stages
+        else if (N == 3072 && K == 768) c = 1;            // fc: 128x64, 8 waves, 3 stages
         if (c >= 0 && cfg_fits(c, K)) return c;
     }
-    const int order[] = {0, 1, 2, 7, 3, 4, 11, 5, 6, 10};
+    const int order[] = {6, 0, 5, 2, 3, 8};
     int last = -1;
     for (int c : order) {
         if (!cfg_fits(c, K)) continue;
@@ -379,7 +601,7 @@ static void launch_gemm(const GemmCfg &g, uint16_t *C, const uint16_t *A, const 
     const int ntiles = tiles_m * tiles_n;
     const int vec = (N % 4 == 0) && (((uintptr_t)C & 7u) == 0);
     auto fn = qw ? g.int8 : g.fp16;
-    hipLaunchKernelGGL(fn, dim3(ntiles), dim3(256), 0, stream(), C, A, W, Ws, bias, M, N, K, tiles_m, ntiles, vec);
+    hipLaunchKernelGGL(fn, dim3(ntiles), dim3(g.threads), 0, stream(), C, A, W, Ws, bias, M, N, K, tiles_m, ntiles, vec);
 }
 
 static bool gemm_args(const char *who, const void *C, const void *A, const void *W, int M, int N, int K) {

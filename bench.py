@@ -118,7 +118,7 @@ def bench_gemm_set(B, steps, warmup):
     achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": None,
-                "kernel": f"k_gemm_mfma<{dom[0]}>", "avg_launch_us": round(d["ms"] / d["launches"] * 1e3, 3),
+                "kernel": dom[0], "avg_launch_us": round(d["ms"] / d["launches"] * 1e3, 3),
                 "flops_per_launch": d["flops"] / d["launches"]}
     roofline.update(measured_traffic(dom[0], [x for x in shapes if x["kernel"] == dom[0]]))
     return flops_step, ms_step, shapes, roofline
@@ -137,11 +137,14 @@ def measured_traffic(cfg_name, shapes):
            (768, 3072): "mlp-proj 512x768x3072"}
     want = [prof["per_shape"].get(key.get((x["N"], x["K"]), ""), {}) for x in shapes]
     import re
-    m = re.fullmatch(r"bn(\d+)_bm(\d+)_bk(\d+)_w(\d+)x(\d+)_d(\d+)", cfg_name)
-    if not m:
-        return {}
-    bn, bm, bk, wn, wm, dep = m.groups()
-    tag = f"k_gemm_mfma<{bn}, {bm}, {bk}, {wn}, {wm}, false, {dep}, false>"
+    m = re.fullmatch(r"dl_bn(\d+)_bm(\d+)_w(\d+)x(\d+)_s(\d+)", cfg_name)
+    if m:
+        tag = "k_gemm_dl<{}, {}, {}, {}, {}, false>".format(*m.groups())
+    else:
+        m = re.fullmatch(r"bn(\d+)_bm(\d+)_bk(\d+)_w(\d+)x(\d+)_d(\d+)", cfg_name)
+        if not m:
+            return {}
+        tag = "k_gemm_mfma<{}, {}, {}, {}, {}, false, {}, false>".format(*m.groups())
     if not want or any(not w or w.get("kernel") != tag for w in want):
         return {}
     return {"traffic": round(sum(w["bytes"] for w in want) / len(want)), "traffic_source": prof["source"]}
