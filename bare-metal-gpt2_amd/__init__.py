@@ -21,6 +21,7 @@ LIB_PATH = os.path.join(HERE, "libgpt2amd.so")
 N_LAYER, N_HEAD, N_EMBD, VOCAB, N_CTX = 12, 12, 768, 50257, 1024
 HEAD_DIM, FFN, QKV = 64, 3072, 2304
 TOTAL_PARAMS = 124439808
+DECODE_AUTO, DECODE_MULTI, DECODE_PERSISTENT = -1, 0, 1   # gpt2_decode_graph_create_mode modes
 N_QTENSORS = 1 + 4 * N_LAYER
 
 _vp = C.c_void_p
@@ -153,6 +154,11 @@ SIGNATURES = {
     "gpt2_gemv_dispatch": (None, [_BE, _vp, _vp, _vp, C.POINTER(GPT2QW), _vp, _i, _i]),
     "gpt2_decode_graph_create": (_vp, [_BE, C.POINTER(GPT2WeightsGPU), C.POINTER(GPT2KVCache),
                                        C.POINTER(GPT2ScratchGPU), _vp, _vp]),
+    "gpt2_decode_graph_create_mode": (_vp, [_BE, C.POINTER(GPT2WeightsGPU), C.POINTER(GPT2KVCache),
+                                            C.POINTER(GPT2ScratchGPU), _vp, _vp, _i]),
+    "gpt2_decode_graph_mode": (_i, [_vp]),
+    "gpt2_tune_decode_spin": (None, [_i]),
+    "gpt2_tune_decode_trace": (None, [_vp]),
     "gpt2_decode_graph_set": (_i, [_vp, _i, _i]),
     "gpt2_decode_graph_run": (_i, [_vp, _i]),
     "gpt2_decode_graph_sync": (_i, [_vp, C.POINTER(C.c_int), C.POINTER(C.c_int)]),

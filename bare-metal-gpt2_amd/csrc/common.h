@@ -64,6 +64,28 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Wave-uniform sum / max: DPP within each 16-lane row, then the four row results are read as
+// scalars (v_readlane) instead of crossing rows through LDS permutes.  Every lane gets the same
+// value; the row results are combined in the fixed order 0, 16, 32, 48.
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ float wave_sum_u(float v) {
+    v = row16_sum(v);
+    return ((lane_f(v, 0) + lane_f(v, 16)) + lane_f(v, 32)) + lane_f(v, 48);
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, true)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, true)));
+    return v;
+}
+__device__ __forceinline__ float wave_max_u(float v) {
+    v = row16_max(v);
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
@@ -74,6 +96,23 @@ __device__ __forceinline__ float h2f(uint16_t h) {
 }
 __device__ __forceinline__ uint16_t f2h(float f) {
     return __builtin_bit_cast(uint16_t, (f16)f);   // v_cvt_f16_f32: round to nearest even
+}
+
+// gelu_new, the tanh form (model/config.h:41-42): 0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))).
+__device__ __forceinline__ float gelu_tanh(float v) {
+    const float z = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+    return 0.5f * v * (1.0f + tanhf(z));
+}
+
+// Sign-exact int8 -> fp16 for four packed bytes: (b ^ 0x80) is b + 128 in [1, 255]; the half with
+// bits 0x6400 | u is 1024 + u; subtracting 1152 leaves b.
+__device__ __forceinline__ void i8x4_to_f16x4_v(uint32_t w, f16x2 &lo, f16x2 &hi) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x05010400u);
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x07030602u);
+    const f16x2 off = {(f16)-1152.0f, (f16)-1152.0f};
+    lo = __builtin_bit_cast(f16x2, a) + off;
+    hi = __builtin_bit_cast(f16x2, b) + off;
 }
 
 }  // namespace g2

@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "common.h"
+#include "decode.h"
 
 namespace g2 {
 void gemv(uint16_t *C, const uint16_t *x, const void *W, const float *Ws, const uint16_t *bias, int N, int K, bool qw,
@@ -370,40 +371,82 @@ struct GPT2DecodeGraph {
     hipStream_t stream;
     hipGraph_t graph;
     hipGraphExec_t exec;
-    int *state;       // device {token, pos}
+    int *state;       // device {token, pos, epoch, error}
     GPT2KVCache *kv;
     int host_pos;     // position the next replay consumes, tracked on the host
+    int mode;         // GPT2_DECODE_MULTI or GPT2_DECODE_PERSISTENT
+    PDPlan plan;      // persistent mode only
+    uint64_t *ll;     // persistent mode: exchange arena
 };
 
-extern "C" GPT2DecodeGraph *gpt2_decode_graph_create(const GPT2Backend *be, const GPT2WeightsGPU *w, GPT2KVCache *kv,
-                                                     GPT2ScratchGPU *s, gpt2_half *logits, int *tokens) {
+static void graph_free(GPT2DecodeGraph *g) {
+    if (g->stream) hipStreamDestroy(g->stream);
+    if (g->mode == GPT2_DECODE_PERSISTENT) persist_free(g->plan);
+    gpt2_dfree(g->ll);
+    gpt2_dfree(g->state);
+    delete g;
+}
+
+extern "C" GPT2DecodeGraph *gpt2_decode_graph_create_mode(const GPT2Backend *be, const GPT2WeightsGPU *w,
+                                                          GPT2KVCache *kv, GPT2ScratchGPU *s, gpt2_half *logits,
+                                                          int *tokens, int mode) {
     if (!be || !w || !w->data || !kv || !kv->data || !s || !logits) { arg_fail("gpt2_decode_graph_create: null argument"); return nullptr; }
+    if (mode == GPT2_DECODE_AUTO) {
+        const char *e = getenv("GPT2_DECODE_PERSISTENT");
+        mode = (e && e[0] == '0') ? GPT2_DECODE_MULTI : GPT2_DECODE_PERSISTENT;
+    }
+    if (mode != GPT2_DECODE_MULTI && mode != GPT2_DECODE_PERSISTENT) { arg_fail("gpt2_decode_graph_create: bad mode"); return nullptr; }
     GPT2DecodeGraph *g = new GPT2DecodeGraph();
     g->kv = kv;
     g->host_pos = kv->len;
-    if (hipStreamCreate(&g->stream) != hipSuccess) { delete g; set_error(E_STATE, "hipStreamCreate"); return nullptr; }
-    g->state = (int *)gpt2_dmalloc(2 * sizeof(int));
-    const int init[2] = {0, kv->len};
-    hipMemcpy(g->state, init, sizeof(init), hipMemcpyHostToDevice);
+    g->mode = GPT2_DECODE_MULTI;
+    if (hipStreamCreate(&g->stream) != hipSuccess) { g->stream = nullptr; graph_free(g); set_error(E_STATE, "hipStreamCreate"); return nullptr; }
+    g->state = (int *)gpt2_dmalloc(4 * sizeof(int));
+    if (!g->state) { graph_free(g); return nullptr; }
+    const int init[4] = {0, kv->len, 1, 0};   // epoch 1: the zeroed exchange arena holds flag 0
+    if (hipMemcpy(g->state, init, sizeof(init), hipMemcpyHostToDevice) != hipSuccess) {
+        graph_free(g);
+        set_error(E_STATE, "decode graph state");
+        return nullptr;
+    }
+    // The persistent step needs this library's fused GEMV path; otherwise the multi-kernel step runs.
+    if (mode == GPT2_DECODE_PERSISTENT && fused_decode_ok(be)) {
+        g->ll = (uint64_t *)gpt2_dmalloc(persist_ll_bytes());
+        if (g->ll && hipMemset(g->ll, 0, persist_ll_bytes()) == hipSuccess &&
+            persist_plan(g->plan, be, w, kv, logits, g->state, tokens, g->ll, g->state + 3))
+            g->mode = GPT2_DECODE_PERSISTENT;
+        else {
+            persist_free(g->plan);
+            gpt2_dfree(g->ll);
+            g->ll = nullptr;
+            gpt2_last_error();   // fall back quietly to the multi-kernel step
+        }
+    }
 
     hipStream_t prev = stream();
     gpt2_set_stream(g->stream);
     hipError_t e = hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal);
     if (e == hipSuccess) {
-        decode_step(be, w, kv, StepArg{0, 0, g->state}, s, logits, nullptr, g->state, tokens);
+        if (g->mode == GPT2_DECODE_PERSISTENT) persist_launch(g->plan, g->stream);
+        else decode_step(be, w, kv, StepArg{0, 0, g->state}, s, logits, nullptr, g->state, tokens);
         e = hipStreamEndCapture(g->stream, &g->graph);
     }
     gpt2_set_stream(prev);
     if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
     if (e != hipSuccess) {
         set_error((int)e, "decode graph capture/instantiate");
-        hipStreamDestroy(g->stream);
-        gpt2_dfree(g->state);
-        delete g;
+        graph_free(g);
         return nullptr;
     }
     return g;
 }
+
+extern "C" GPT2DecodeGraph *gpt2_decode_graph_create(const GPT2Backend *be, const GPT2WeightsGPU *w, GPT2KVCache *kv,
+                                                     GPT2ScratchGPU *s, gpt2_half *logits, int *tokens) {
+    return gpt2_decode_graph_create_mode(be, w, kv, s, logits, tokens, GPT2_DECODE_AUTO);
+}
+
+extern "C" int gpt2_decode_graph_mode(const GPT2DecodeGraph *g) { return g ? g->mode : -1; }
 
 extern "C" int gpt2_decode_graph_set(GPT2DecodeGraph *g, int token, int pos) {
     if (!g || token < 0 || token >= GPT2_VOCAB || pos < 0 || pos >= g->kv->maxT) { set_error(E_ARG, "gpt2_decode_graph_set"); return 1; }
@@ -428,10 +471,15 @@ extern "C" int gpt2_decode_graph_run(GPT2DecodeGraph *g, int steps) {
 
 extern "C" int gpt2_decode_graph_sync(GPT2DecodeGraph *g, int *token, int *pos) {
     if (!g) return 1;
-    int st[2];
+    int st[4];
     hipError_t e = hipMemcpyAsync(st, g->state, sizeof(st), hipMemcpyDeviceToHost, g->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(g->stream);
     if (e != hipSuccess) { set_error((int)e, "gpt2_decode_graph_sync"); return (int)e; }
+    if (st[3]) {
+        // A persistent step gave up waiting for another work-group's output: its results are void.
+        set_error(E_STATE, "persistent decode step: an exchange timed out (work-groups not co-resident?)");
+        return E_STATE;
+    }
     if (token) *token = st[0];
     if (pos) *pos = st[1];
     g->kv->len = st[1];
@@ -462,9 +510,7 @@ extern "C" void gpt2_decode_graph_destroy(GPT2DecodeGraph *g) {
     hipStreamSynchronize(g->stream);
     hipGraphExecDestroy(g->exec);
     hipGraphDestroy(g->graph);
-    hipStreamDestroy(g->stream);
-    gpt2_dfree(g->state);
-    delete g;
+    graph_free(g);
 }
 
 // ============================================================================ INT8 weights

@@ -19,14 +19,6 @@
 
 namespace g2 {
 
-__device__ __forceinline__ void i8x4_to_f16x4_v(uint32_t w, f16x2 &lo, f16x2 &hi) {
-    const uint32_t u = w ^ 0x80808080u;
-    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x05010400u);
-    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x07030602u);
-    const f16x2 off = {(f16)-1152.0f, (f16)-1152.0f};
-    lo = __builtin_bit_cast(f16x2, a) + off;
-    hi = __builtin_bit_cast(f16x2, b) + off;
-}
 
 __device__ __forceinline__ float dot8(const i32x4 w, const f16x8 x, float acc) {
     const f16x8 wh = __builtin_bit_cast(f16x8, w);
@@ -66,10 +58,6 @@ __device__ __forceinline__ float slot_sum(float v) {
 // Epilogues a decode step fuses into its GEMVs.
 enum { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2 };
 
-__device__ __forceinline__ float gelu_tanh(float v) {
-    const float z = 0.7978845608028654f * (v + 0.044715f * v * v * v);
-    return 0.5f * v * (1.0f + tanhf(z));
-}
 
 // LPR lanes per row, CPL 16-byte chunks per lane (row = LPR*CPL chunks), U rows per slot in flight.
 // LN: x is the residual stream and the kernel applies LayerNorm(x; ln_g, ln_b) to it first.  The

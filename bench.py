@@ -247,19 +247,32 @@ def bench_decode(B, steady_reps=64):
     L.gpt2_sync()
     pkg.check("prefill")
     first = int(np.argmax(pkg.half_bits_to_f32(logits.numpy(np.uint16, (VOCAB,)))))
-    g = L.gpt2_decode_graph_create(be, C.byref(model.gpu), C.byref(kv.kv), C.byref(scr.s), logits.ptr, tokens.ptr)
-    if not g:
-        pkg.check("graph create")
-        raise RuntimeError("graph create failed")
     ms = C.c_float()
-    # steady state at pos 512 (cache length 512): each replay is re-pinned to pos 512
-    samples = []
-    for i in range(steady_reps + 5):
-        L.gpt2_decode_graph_set(g, first, P)
-        L.gpt2_decode_graph_time(g, 1, C.byref(ms))
-        if i >= 5:
-            samples.append(ms.value)
-    pkg.check("steady decode")
+
+    def steady(mode):
+        """Median ms per replay at pos 512 (cache length 512), each replay re-pinned to pos 512."""
+        g = L.gpt2_decode_graph_create_mode(be, C.byref(model.gpu), C.byref(kv.kv), C.byref(scr.s), logits.ptr,
+                                            tokens.ptr, mode)
+        if not g:
+            pkg.check("graph create")
+            raise RuntimeError("graph create failed")
+        got_mode = L.gpt2_decode_graph_mode(g)
+        samples = []
+        for i in range(steady_reps + 5):
+            L.gpt2_decode_graph_set(g, first, P)
+            L.gpt2_decode_graph_time(g, 1, C.byref(ms))
+            if i >= 5:
+                samples.append(ms.value)
+        tok, pos = C.c_int(), C.c_int()
+        if L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)):
+            pkg.check("steady decode")
+        pkg.check("steady decode")
+        return g, got_mode, samples
+
+    # multi-kernel captured step (reference point), then the persistent step (the default)
+    g_multi, _, samples_multi = steady(pkg.DECODE_MULTI)
+    L.gpt2_decode_graph_destroy(g_multi)
+    g, mode, samples = steady(pkg.DECODE_AUTO)
     # eager (non-graph) step at the same position, for the launch-overhead comparison
     eager = []
     for i in range(12):
@@ -272,17 +285,22 @@ def bench_decode(B, steady_reps=64):
             eager.append((time.perf_counter() - t) * 1e3)
     pkg.check("eager decode")
     # the full greedy run: 511 steps from pos 512 (ctx 512 -> 1023)
+    kv.kv.len = P
     L.gpt2_decode_graph_set(g, first, P)
     L.gpt2_decode_graph_time(g, 511, C.byref(ms))
     tok, pos = C.c_int(), C.c_int()
-    L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos))
+    if L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)):
+        pkg.check("greedy run")
     pkg.check("greedy run")
     L.gpt2_decode_graph_destroy(g)
     streamed = model.q.streamed_bytes
     kv_bytes = L.gpt2_kv_step_bytes(C.byref(kv.kv), P + 1)
     med = float(np.median(samples))
-    res = {"tok_s_at_512": round(1000.0 / med, 1), "ms_step_at_512": round(med, 4),
+    med_multi = float(np.median(samples_multi))
+    res = {"step": "persistent (one kernel per token)" if mode == pkg.DECODE_PERSISTENT else "multi-kernel graph",
+           "tok_s_at_512": round(1000.0 / med, 1), "ms_step_at_512": round(med, 4),
            "ms_step_min_max": [round(min(samples), 4), round(max(samples), 4)],
+           "multi_kernel_graph_tok_s_at_512": round(1000.0 / med_multi, 1),
            "eager_ms_step_at_512": round(float(np.median(eager)), 4),
            "greedy_511_tok_s": round(1000.0 / ms.value, 1), "greedy_final_pos": pos.value,
            "weight_bytes": int(streamed), "kv_bytes_at_513": int(kv_bytes),

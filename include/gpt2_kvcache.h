@@ -69,6 +69,25 @@ void gpt2_gemv_dispatch(const GPT2Backend *be, gpt2_half *C, const gpt2_half *A,
 typedef struct GPT2DecodeGraph GPT2DecodeGraph;
 GPT2DecodeGraph *gpt2_decode_graph_create(const GPT2Backend *be, const GPT2WeightsGPU *w, GPT2KVCache *kv,
                                           GPT2ScratchGPU *s, gpt2_half *logits, int *tokens);
+/* How the captured step runs:
+ *   GPT2_DECODE_MULTI       the step's kernels one after another (~62 launches per token);
+ *   GPT2_DECODE_PERSISTENT  one persistent kernel per token: 256 work-groups run every phase of the
+ *                           step and exchange the small activation vectors through coherent
+ *                           flag words instead of kernel boundaries.  Needs this library's GEMV
+ *                           backend slots (int8 / gemv backends) and the GPU to itself while a step
+ *                           runs (its work-groups must be resident together; if they are not, the
+ *                           step gives up after a bounded wait and gpt2_decode_graph_sync reports
+ *                           an error);
+ *   GPT2_DECODE_AUTO        persistent when the backend allows it (env GPT2_DECODE_PERSISTENT=0
+ *                           forces the multi-kernel step).
+ * gpt2_decode_graph_create uses GPT2_DECODE_AUTO.  No reference counterpart. */
+#define GPT2_DECODE_AUTO (-1)
+#define GPT2_DECODE_MULTI 0
+#define GPT2_DECODE_PERSISTENT 1
+GPT2DecodeGraph *gpt2_decode_graph_create_mode(const GPT2Backend *be, const GPT2WeightsGPU *w, GPT2KVCache *kv,
+                                               GPT2ScratchGPU *s, gpt2_half *logits, int *tokens, int mode);
+/* The mode the graph actually runs (a persistent request falls back to GPT2_DECODE_MULTI). */
+int gpt2_decode_graph_mode(const GPT2DecodeGraph *g);
 /* Set the device-side state: next step consumes `token` at position `pos` (kv must hold pos rows). */
 int gpt2_decode_graph_set(GPT2DecodeGraph *g, int token, int pos);
 /* Replay `steps` steps back to back on the graph's stream; no host synchronisation inside. Steps

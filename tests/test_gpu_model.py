@@ -6,8 +6,11 @@ bench/kv_gate.cu:114-138), applied to the fp16 engine against the fp32 CPU oracl
   max KL(softmax(ref) || softmax(got)) < 0.02 over the logits rows (gate (c)),
   cached decode == no-KV recompute within fp16 noise (the [EQ] gate).
 INT8 runs are compared with the oracle on the dequantized weights (tools/dequant_check.py).
-The graph-replayed decode uses the same kernels in the same order as the eager step, so its tokens
-and logits must match the eager loop bit for bit.
+The multi-kernel graph decode uses the same kernels in the same order as the eager step, so its
+tokens and logits must match the eager loop bit for bit.  The persistent decode step (one kernel per
+token) sums in a different order, so it is held to the same fp16 gates against the eager step, and
+to exactness where its own logic decides (the greedy token is the first argmax of its own logits,
+replays are deterministic).
 """
 import ctypes as C
 
@@ -248,10 +251,11 @@ def test_graph_decode_matches_eager(pkg, L, synth, model, backend):
         # graph: same cache prefix (positions >= P are rewritten by the replays)
         kv.kv.len = P
         tokens = pkg.Dev(1024 * 4)
-        g = L.gpt2_decode_graph_create(pkg.backend(backend), C.byref(model.gpu), C.byref(kv.kv), C.byref(scr.s),
-                                       logits.ptr, tokens.ptr)
+        g = L.gpt2_decode_graph_create_mode(pkg.backend(backend), C.byref(model.gpu), C.byref(kv.kv),
+                                            C.byref(scr.s), logits.ptr, tokens.ptr, pkg.DECODE_MULTI)
         assert g, pkg.check("graph create")
         try:
+            assert L.gpt2_decode_graph_mode(g) == pkg.DECODE_MULTI
             assert L.gpt2_decode_graph_set(g, first, P) == 0
             # replay one step at a time, with unrelated eager work and syncs between replays
             junk_a, junk_c = pkg.Dev(64 * 768 * 2), pkg.Dev(64 * 2304 * 2)
@@ -284,3 +288,136 @@ def test_graph_decode_matches_eager(pkg, L, synth, model, backend):
             L.gpt2_quant_free(C.byref(model.q))
             model.q = None
             model.gpu.q = None
+
+
+def first_argmax(lg16):
+    """Greedy token as the step defines it: the lowest index among the maxima of the fp16 logits."""
+    return int(np.argmax(oracle.f16_to_f32(lg16)))
+
+
+@pytest.mark.parametrize("backend", ["int8", "gemv"])
+def test_persistent_decode_matches_eager(pkg, L, synth, model, backend):
+    """One-kernel-per-token decode against the eager multi-kernel step, teacher-forced: before every
+    replay the graph state is set to the eager run's (token, pos), so each step starts from the same
+    cache prefix and input token.  Gates: rel_err <= 1e-2 and KL < 2e-3 per step against the eager
+    logits; the step's own greedy token equals the first argmax of its own logits exactly."""
+    if backend == "int8":
+        model.quantize()
+    try:
+        ids = synth.token_ids(40, seed=18)
+        P, n = len(ids), 20
+        kv, scr, logits = decode_setup(pkg, L, model, ids, backend)
+        first = first_argmax(logits.numpy(np.uint16, (V,)))
+        eager_toks, eager_rows = eager_greedy(pkg, L, model, kv, scr, logits, backend, first, P, n)
+        feed = [first] + eager_toks[:-1]
+        kv.kv.len = P
+        tokens = pkg.Dev(1024 * 4)
+        g = L.gpt2_decode_graph_create_mode(pkg.backend(backend), C.byref(model.gpu), C.byref(kv.kv),
+                                            C.byref(scr.s), logits.ptr, tokens.ptr, pkg.DECODE_PERSISTENT)
+        assert g, pkg.check("graph create")
+        try:
+            assert L.gpt2_decode_graph_mode(g) == pkg.DECODE_PERSISTENT
+            tok, pos = C.c_int(), C.c_int()
+            for i in range(n):
+                assert L.gpt2_decode_graph_set(g, feed[i], P + i) == 0
+                assert L.gpt2_decode_graph_run(g, 1) == 0
+                assert L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)) == 0, pkg.check("persistent step")
+                assert pos.value == P + i + 1
+                lg = logits.numpy(np.uint16, (V,))
+                got, ref = oracle.f16_to_f32(lg)[None], oracle.f16_to_f32(eager_rows[i])[None]
+                assert rel_err(got, ref) <= 1e-2, (i, rel_err(got, ref))
+                assert kl_rows(ref, got).max() < 2e-3, i
+                assert tok.value == first_argmax(lg), i
+                assert tokens.numpy(np.int32, (1024,))[P + i + 1] == tok.value
+            assert kv.kv.len == P + n
+        finally:
+            L.gpt2_decode_graph_destroy(g)
+        pkg.check("persistent graph")
+        scr.free()
+        kv.free()
+    finally:
+        if backend == "int8":
+            L.gpt2_quant_free(C.byref(model.q))
+            model.q = None
+            model.gpu.q = None
+
+
+def test_persistent_decode_deterministic_free_run(pkg, L, synth, model):
+    """Two free-running greedy replays of the persistent step from the same state produce the same
+    tokens and the same final logits bit for bit (fixed reduction orders, no atomics in the math),
+    and a replay re-pinned to an already used position is not confused by the previous epoch."""
+    model.quantize()
+    try:
+        ids = synth.token_ids(32, seed=19)
+        P, n = len(ids), 16
+        kv, scr, logits = decode_setup(pkg, L, model, ids, "int8")
+        first = first_argmax(logits.numpy(np.uint16, (V,)))
+        tokens = pkg.Dev(1024 * 4)
+        g = L.gpt2_decode_graph_create_mode(pkg.backend("int8"), C.byref(model.gpu), C.byref(kv.kv),
+                                            C.byref(scr.s), logits.ptr, tokens.ptr, pkg.DECODE_PERSISTENT)
+        assert g, pkg.check("graph create")
+        try:
+            runs = []
+            for _ in range(2):
+                tok, pos = C.c_int(), C.c_int()
+                assert L.gpt2_decode_graph_set(g, first, P) == 0
+                assert L.gpt2_decode_graph_run(g, n) == 0
+                assert L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)) == 0, pkg.check("free run")
+                assert pos.value == P + n
+                runs.append((list(tokens.numpy(np.int32, (1024,))[P + 1:P + n + 1]), logits.numpy(np.uint16, (V,))))
+            assert runs[0][0] == runs[1][0]
+            assert np.array_equal(runs[0][1], runs[1][1])
+            assert runs[0][0][-1] == first_argmax(runs[0][1])
+        finally:
+            L.gpt2_decode_graph_destroy(g)
+        scr.free()
+        kv.free()
+    finally:
+        L.gpt2_quant_free(C.byref(model.q))
+        model.q = None
+        model.gpu.q = None
+
+
+def test_persistent_decode_falls_back_without_gemv(pkg, L, synth, model):
+    """Backends without this library's GEMV slots (flash: M=1 matmul fallback) get the multi-kernel
+    step even when the persistent one is requested."""
+    ids = synth.token_ids(8, seed=20)
+    kv, scr, logits = decode_setup(pkg, L, model, ids, "flash")
+    tokens = pkg.Dev(1024 * 4)
+    g = L.gpt2_decode_graph_create_mode(pkg.backend("flash"), C.byref(model.gpu), C.byref(kv.kv), C.byref(scr.s),
+                                        logits.ptr, tokens.ptr, pkg.DECODE_PERSISTENT)
+    assert g, pkg.check("graph create")
+    try:
+        assert L.gpt2_decode_graph_mode(g) == pkg.DECODE_MULTI
+    finally:
+        L.gpt2_decode_graph_destroy(g)
+    scr.free()
+    kv.free()
+
+
+def test_persistent_decode_timeout_is_reported(pkg, L, synth, model):
+    """Error path forced from the host: with a zero-round poll limit a work-group gives up at the
+    first exchange word that has not arrived yet, every work-group still exits, and the sync call
+    reports the failure instead of returning a token."""
+    ids = synth.token_ids(8, seed=21)
+    kv, scr, logits = decode_setup(pkg, L, model, ids, "gemv")
+    tokens = pkg.Dev(1024 * 4)
+    L.gpt2_tune_decode_spin(0)
+    try:
+        g = L.gpt2_decode_graph_create_mode(pkg.backend("gemv"), C.byref(model.gpu), C.byref(kv.kv),
+                                            C.byref(scr.s), logits.ptr, tokens.ptr, pkg.DECODE_PERSISTENT)
+    finally:
+        L.gpt2_tune_decode_spin(-1)
+    assert g, pkg.check("graph create")
+    try:
+        assert L.gpt2_decode_graph_mode(g) == pkg.DECODE_PERSISTENT
+        tok, pos = C.c_int(), C.c_int()
+        assert L.gpt2_decode_graph_set(g, 5, len(ids)) == 0
+        assert L.gpt2_decode_graph_run(g, 1) == 0
+        assert L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)) != 0
+        assert L.gpt2_last_error() != 0
+    finally:
+        L.gpt2_decode_graph_destroy(g)
+    L.gpt2_last_error()
+    scr.free()
+    kv.free()
