@@ -115,7 +115,25 @@ __device__ __forceinline__ void i8x4_to_f16x4_v(uint32_t w, f16x2 &lo, f16x2 &hi
     hi = __builtin_bit_cast(f16x2, b) + off;
 }
 
+// Work-group barrier for LDS traffic: waits for this wave's LDS (and scalar) operations only, not for
+// its outstanding global loads and stores, which __syncthreads() also drains.  Loads issued ahead
+// (the next tile, the next phase's weights) stay in flight across it; the caller waits for those
+// itself before using them.  The "memory" clobber keeps the compiler from moving memory accesses
+// across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// s_waitcnt immediate for "at most n vector-memory operations outstanding" (gfx9 encoding, expcnt
+// and lgkmcnt left unconstrained).
+template <int n>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
+}
+
 }  // namespace g2
+
+// LDS pointer for global_load_lds (device pass only: the address space does not exist on the host).
+#define G2_LDS(p) ((__attribute__((address_space(3))) void *)(p))
 
 #define G2_HALF(p) reinterpret_cast<f16 *>(p)
 #define G2_CHALF(p) reinterpret_cast<const f16 *>(p)

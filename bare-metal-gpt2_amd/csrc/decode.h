@@ -14,8 +14,10 @@ struct PDLayer {
     const uint16_t *b[4];
 };
 
+// Passed by value as the kernel argument (~1.7 KB): the per-layer pointers are then read with
+// scalar loads from the argument segment, which never wait behind the step's in-flight vector loads.
 struct PDArgs {
-    const PDLayer *layers;            // device array [12]
+    PDLayer layers[GPT2_N_LAYER];
     const uint16_t *wte, *wpe, *lnf_g, *lnf_b;
     const void *head_w;               // tied head: fp16 wte, or int8 codes when head_s != nullptr
     const float *head_s;
@@ -32,15 +34,13 @@ struct PDArgs {
 
 struct PDPlan {
     PDArgs args;
-    PDLayer *d_layers;
+    bool q8;                          // int8 layer matrices (else fp16)
 };
 
-// Builds the step's argument block (and uploads the per-layer table); false when the backend or
-// weights need the multi-kernel step.
+// Builds the step's argument block; false when the backend or weights need the multi-kernel step.
 bool persist_plan(PDPlan &p, const GPT2Backend *be, const GPT2WeightsGPU *w, GPT2KVCache *kv, uint16_t *logits,
                   int *state, int *tokens, uint64_t *ll, int *err);
 void persist_launch(const PDPlan &p, hipStream_t s);
 size_t persist_ll_bytes();
-void persist_free(PDPlan &p);
 
 }  // namespace g2

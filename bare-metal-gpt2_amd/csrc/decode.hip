@@ -6,26 +6,38 @@
 // cost ~350 us while its weights (162 MB) stream from HBM in ~30 us.
 //
 // Design:
-//   * PD_G work-groups (one per CU) run the whole step.  Work is split by output rows in every
-//     phase; 12 layers x {LN1+QKV, attention, proj+residual, LN2+fc+gelu, mlp-proj+residual}, then
-//     LN_f + tied head + argmax.
+//   * PD_G work-groups (one per CU) run the whole step, in four phases per layer:
+//       A  48 attention work-groups, four per head (key splits): LN1 of x, the head's q and the
+//          split's 16-row slices of k and v of the new key (96 weight rows, staged in LDS by DMA
+//          during the previous layer), the K/V append, attention over the split's share of the
+//          earlier keys; they send an unnormalized partial (m, l, c[64]) plus the slice's part of
+//          q.k_new and its v_new slice.
+//       P  192 GEMV work-groups: combine the partials (the new key is one more partial), proj rows,
+//          + bias + residual.
+//       F  the same work-groups: LN2, fc rows, gelu.
+//       M  the same work-groups: mlp-proj rows + bias + residual.
+//     then LN_f + tied head + argmax on every work-group, and work-group 0 picks the token.
 //   * Phases exchange their (small) output vectors through "flag words": 64-bit words holding 32 bits
 //     of data and the 32-bit sequence number of the phase that wrote them, stored and loaded with
 //     agent-scope (coherent, sc1) atomic accesses.  A consumer polls the words it needs until every
 //     flag matches; there is no fence, no counter and no grid barrier (measured: a fenced grid barrier
-//     costs 16 us at 256 work-groups, a flag-word phase ~2.3 us).  64-bit accesses are single-copy
-//     atomic, so data and flag arrive together.
-//   * Each phase issues its weight loads (straight into registers) before it polls for its input,
-//     so HBM latency hides behind the exchange.
+//     costs 16 us at 256 work-groups, a flag-word exchange ~1.5-2.5 us).  64-bit accesses are
+//     single-copy atomic, so data and flag arrive together.
+//   * Every phase's weights are in flight before its input arrives: GEMV rows go to registers one
+//     phase ahead (issued right after the previous poll completed, so a poll never queues behind
+//     them), the attention work-groups' q/k/v rows go to LDS a layer ahead.  Barriers between waves
+//     wait for LDS traffic only, so they do not drain those loads; per-layer pointers come from the
+//     kernel argument segment (scalar loads) and fp16 parameters stay unconverted until used, since
+//     either would otherwise make the wave wait for every load it has in flight.
 //   * Sequence numbers are epoch*64 + phase, with the epoch a device counter advanced once per token,
 //     so buffers are reused without clearing and a replay at a repeated position cannot match a
-//     stale word.  Every buffer is rewritten only after all of its readers have provably finished
-//     (each phase reads the complete output of the phase before it).
+//     stale word.  A work-group polls a buffer only in a phase it also writes from, so every writer
+//     of a buffer's next version has first read everything the previous version's readers needed.
 //   * Every poll is bounded; on timeout (or once another work-group reported one) the work-group
 //     records an error in `err` and leaves, so the kernel always terminates.
 //   * KV rows of this token are appended to the cache with ordinary stores; later tokens read them
-//     in later launches (kernel boundaries make them visible), this token's attention reads its own
-//     key/value from the exchanged qkv vector.
+//     in later launches (kernel boundaries make them visible); this token's attention takes the new
+//     key and value from the exchanged words instead.
 //
 // Numerics follow the multi-kernel fused step: fp16 activations between phases, fp32 inside,
 // LayerNorm with biased variance and eps inside the sqrt, gelu_new, scale after the fp32 sum then
@@ -40,29 +52,56 @@
 
 namespace g2 {
 
-constexpr int PD_G = 256;                          // work-groups
+constexpr int PD_G = 256;                          // work-groups (one per CU)
 constexpr int PD_T = 256;                          // threads per work-group (4 waves)
-constexpr int PD_S = 2;                            // key splits per head (attention work-groups: H*S)
-constexpr int PD_NC = 2;                           // 64-key chunks per attention wave
-constexpr int PD_E = GPT2_N_EMBD, PD_Q = GPT2_QKV_DIM, PD_F = GPT2_FFN_DIM, PD_V = GPT2_VOCAB;
+constexpr int PD_E = GPT2_N_EMBD, PD_F = GPT2_FFN_DIM, PD_V = GPT2_VOCAB;
 constexpr int PD_D = GPT2_HEAD_DIM, PD_H = GPT2_N_HEAD;
-constexpr int PD_PW = 2 + PD_D;                    // words per attention partial: m, l, c[64]
-constexpr int RQ = PD_Q / PD_G, RP = PD_E / PD_G, RF = PD_F / PD_G, RM = PD_E / PD_G;
+constexpr int PD_S = 4;                            // attention work-groups (key splits) per head
+constexpr int PD_NA = PD_H * PD_S;                 // attention work-groups: 0 .. NA-1
+constexpr int PD_NG = PD_G - PD_NA;                // GEMV work-groups: NA .. G-1
+constexpr int KS = PD_D / PD_S;                    // k and v rows of key `pos` per attention work-group
+constexpr int QR = PD_D + 2 * KS;                  // rows it computes: q (64), its k slice, its v slice
+constexpr int PD_PW = 2 + PD_D + 1 + KS;           // words it sends: m, l, c[64], its q.k part, its v slice
+constexpr int RP = 4, RF = 16, RM = 4;             // rows per GEMV work-group: proj, fc, mlp-proj
+constexpr int PD_NW = PD_E / RP;                   // GEMV work-groups with rows (the rest wait for the head)
 constexpr int RH = (PD_V + PD_G - 1) / PD_G;       // head rows per work-group (the last has fewer)
-static_assert(RQ * PD_G == PD_Q && RP * PD_G == PD_E && RF * PD_G == PD_F, "rows split evenly");
+static_assert(PD_E % RP == 0 && PD_F % RF == 0 && PD_E / RP == PD_F / RF && RM == RP && PD_NW <= PD_NG,
+              "the same GEMV work-groups hold proj, fc and mlp-proj rows");
 static_assert(RF % 2 == 0, "fc rows are exchanged in pairs");
+static_assert(QR % 32 == 0, "the q/k/v GEMV takes two 16-row passes at a time");
 static_assert(PD_G == PD_T, "the final argmax gives each thread one work-group's candidate");
-static_assert(PD_H * PD_S <= PD_G, "one work-group per attention split");
-static_assert(PD_S * 4 * 64 * PD_NC >= GPT2_N_CTX, "the attention waves cover every key of a full cache");
+static_assert(PD_S * 4 * 64 >= GPT2_N_CTX, "an attention wave holds at most 64 keys of a full cache");
 
 // Exchange arena (64-bit flag words).
 constexpr int LL_X = 0;                            // residual stream: 768 words, one fp16 each
-constexpr int LL_QKV = LL_X + PD_E;                // qkv: 2304 words, one fp16 each
-constexpr int LL_ATT = LL_QKV + PD_Q;              // attention partials: H*S*66 words, fp32
-constexpr int LL_HID = LL_ATT + PD_H * PD_S * PD_PW;  // gelu(fc): 1536 words, two fp16 each
+constexpr int LL_ATT = LL_X + PD_E;                // attention: NA*PW words, fp32
+constexpr int LL_HID = LL_ATT + PD_NA * PD_PW;     // gelu(fc): 1536 words, two fp16 each
 constexpr int LL_CAND = LL_HID + PD_F / 2;         // argmax candidates: G words
 constexpr int LL_WORDS = LL_CAND + PD_G;
 constexpr int PD_SPIN = 1 << 15;                   // default poll rounds before a work-group gives up
+// Phase numbers (sequence = epoch*64 + phase): per layer l, 4l attention, 4l+1 x after proj,
+// 4l+2 gelu(fc), 4l+3 x after mlp-proj; 48 head candidates.
+constexpr int PH_CAND = 4 * GPT2_N_LAYER;
+
+// LDS layout (bytes).  Common: xs, xn, argmax scratch.  Attention work-groups: the q/k/v weight rows
+// they compute (QR rows, int8 or fp16), reused after the GEMV for the attention scratch; GEMV
+// work-groups: gelu(fc) and the attention words.
+constexpr int LDS_XS = 0, LDS_XN = LDS_XS + 2 * PD_E, LDS_MISC = LDS_XN + 2 * PD_E;   // misc: 512 B
+constexpr int LDS_ROLE = LDS_MISC + 512;
+template <bool Q8> struct Lds {
+    static constexpr int RB = Q8 ? PD_E : 2 * PD_E;       // bytes per q/k/v weight row
+    static constexpr int W = LDS_ROLE;                    // A: q/k/v weights, QR * RB
+    static constexpr int QKVH = W + QR * RB;              // A: q, k slice, v slice (fp16)
+    static constexpr int QSB = QKVH + 2 * QR;             // A: their scales and biases (fp32)
+    static constexpr int CL = W;                          // A, after the GEMV: [4][64][8] fp32
+    static constexpr int PL = CL + 4 * PD_D * 8 * 4;      // A, after the GEMV: [4][64] fp32
+    static constexpr int HS = LDS_ROLE;                   // G: gelu(fc), 3072 fp16
+    static constexpr int PART = HS + 2 * PD_F;            // G: NA*PW fp32
+    static constexpr int CANDS = LDS_ROLE;                // head phase: G candidates
+    static constexpr int BYTES = QSB + 2 * 4 * QR;
+    static_assert(PART + 4 * PD_NA * PD_PW <= BYTES && PL + 4 * 4 * 64 <= QKVH, "LDS layout");
+    static_assert(BYTES <= 160 * 1024, "fits the 160 KB of LDS of a gfx950 CU");
+};
 
 __device__ __forceinline__ uint64_t ll_ld(const uint64_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -187,61 +226,69 @@ template <int K, bool Q8, int ROWS>
 struct PhaseW {
     static constexpr int J = (ROWS + 3) / 4;
     RowW<K, Q8> r[J];
-    float s[J], b[J];
+    float s[J];
+    uint16_t b[J];   // fp16 bits, converted where used (a conversion here would wait for the load)
 };
 
 template <int K, bool Q8, int ROWS>
 __device__ __forceinline__ void load_phase(PhaseW<K, Q8, ROWS> &P, const void *W, const float *S, const uint16_t *B,
-                                           int r0, int wave, int lane) {
+                                           int r0, int wave, int lane, int limit = ROWS) {
 #pragma unroll
     for (int j = 0; j < PhaseW<K, Q8, ROWS>::J; ++j) {
         const int k = wave + 4 * j;
-        if (k < ROWS) {
+        if (k < ROWS && k < limit) {
             load_row<K, Q8>(P.r[j], W, r0 + k, lane);
             P.s[j] = Q8 ? S[r0 + k] : 1.0f;
-            P.b[j] = B ? h2f(B[r0 + k]) : 0.0f;
+            P.b[j] = B[r0 + k];
         }
     }
 }
 
 // acc * scale + bias for each of the wave's rows; out(k, value) gets the row index inside the share.
 template <int K, bool Q8, int ROWS, class Out>
-__device__ __forceinline__ void run_phase(const PhaseW<K, Q8, ROWS> &P, const f16 *x, int wave, int lane, Out out) {
+__device__ __forceinline__ void run_phase(const PhaseW<K, Q8, ROWS> &P, const f16 *x, int wave, int lane, Out out,
+                                          int limit = ROWS) {
     constexpr int J = PhaseW<K, Q8, ROWS>::J;
     float acc[J];
 #pragma unroll
-    for (int j = 0; j < J; ++j) acc[j] = (wave + 4 * j < ROWS) ? dot_row<K, Q8>(P.r[j], x, lane) : 0.f;
+    for (int j = 0; j < J; ++j) {
+        const int k = wave + 4 * j;
+        acc[j] = (k < ROWS && k < limit) ? dot_row<K, Q8>(P.r[j], x, lane) : 0.f;
+    }
 #pragma unroll
     for (int j = 0; j < J; ++j) acc[j] = wave_sum_u(acc[j]);   // independent reductions, interleaved
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int k = wave + 4 * j;
-        if (k < ROWS) out(k, acc[j] * P.s[j] + P.b[j]);
+        if (k < ROWS && k < limit) out(k, acc[j] * P.s[j] + h2f(P.b[j]));
     }
 }
 
 // LayerNorm of the 768-vector xs into xn (fp16): every wave computes the statistics (same order,
-// same result), then thread t writes elements t, t+256, t+512.
+// same result; lane l sums elements 12l .. 12l+11), then thread t writes elements t, t+256, t+512.
 // gamma and beta of the thread's three elements, loaded before the phase's input arrives.
 struct LNParams {
-    float g[3], b[3];
+    uint16_t g[3], b[3];   // fp16 bits: converting at load time would make the load wait at once
 };
 __device__ __forceinline__ void load_ln(LNParams &p, const uint16_t *g, const uint16_t *b) {
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const int e = threadIdx.x + PD_T * i;
-        p.g[i] = h2f(g[e]);
-        p.b[i] = h2f(b[e]);
+        p.g[i] = g[e];
+        p.b[i] = b[e];
     }
 }
 
 __device__ __forceinline__ void layernorm768(f16 *xn, const f16 *xs, const LNParams &p, int lane) {
     float v[12], s = 0.f;
 #pragma unroll
-    for (int i = 0; i < 12; ++i) {
-        v[i] = (float)xs[lane + 64 * i];
-        s += v[i];
+    for (int i = 0; i < 3; ++i) {
+        const f16x4 x4 = *reinterpret_cast<const f16x4 *>(xs + 12 * lane + 4 * i);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[4 * i + t] = (float)x4[t];
     }
+#pragma unroll
+    for (int i = 0; i < 12; ++i) s += v[i];
     const float mean = wave_sum_u(s) * (1.0f / PD_E);
     float q = 0.f;
 #pragma unroll
@@ -253,24 +300,43 @@ __device__ __forceinline__ void layernorm768(f16 *xn, const f16 *xs, const LNPar
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const int e = threadIdx.x + PD_T * i;
-        xn[e] = (f16)(((float)xs[e] - mean) * rstd * p.g[i] + p.b[i]);
+        xn[e] = (f16)(((float)xs[e] - mean) * rstd * h2f(p.g[i]) + h2f(p.b[i]));
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // ------------------------------------------------------------------------------ the step
+// Row r of the q/k/v rows attention work-group (h, sp) computes: q rows 0-63 of head h, then k and
+// v rows [KS*sp, KS*sp + KS) of head h, as row indices of the [3*768][768] c_attn weight.
+__device__ __forceinline__ int qkv_row(int h, int sp, int r) {
+    return r < PD_D ? h * PD_D + r
+                    : (r < PD_D + KS ? PD_E : 2 * PD_E) + h * PD_D + KS * sp + ((r - PD_D) & (KS - 1));
+}
+
+// DMA of those QR weight rows (RB bytes each) into LDS, row-major: 1 KB per wave instruction, lane i
+// of instruction q landing at byte 1024q + 16i.
+template <int RB>
+__device__ __forceinline__ void dma_qkv(char *lds_w, const void *W, int h, int sp, int wave, int lane) {
+    constexpr int NINS = QR * RB / 1024;
+    static_assert(QR * RB % 1024 == 0 && RB % 16 == 0, "whole 1 KB DMA blocks of whole 16 B pieces");
+    const char *Wb = reinterpret_cast<const char *>(W);
+    for (int q = wave; q < NINS; q += 4) {
+        const int byte = q * 1024 + lane * 16, r = byte / RB, off = byte - r * RB;
+        __builtin_amdgcn_global_load_lds(Wb + (size_t)qkv_row(h, sp, r) * RB + off, G2_LDS(lds_w + q * 1024), 16, 0, 0);
+    }
+}
+
+// Q8: every layer matrix is int8 codes with per-row scales (else every one is fp16).
+template <bool Q8>
 __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
-    __shared__ __attribute__((aligned(16))) f16 xs[PD_E];     // current residual stream
-    __shared__ __attribute__((aligned(16))) f16 xn[PD_E];     // normalized input / attention output
-    __shared__ __attribute__((aligned(16))) f16 hs[PD_F];     // gelu(fc) for the mlp-proj phase
-    __shared__ __attribute__((aligned(16))) float part[PD_H * PD_S * PD_PW];
-    __shared__ __attribute__((aligned(16))) f16 qkvh[3 * PD_D];  // q, k, v of one head
-    __shared__ float sm[4], sl[4];
-    __shared__ __attribute__((aligned(16))) float cl[4][PD_D][8];      // attention: [wave][dim][key slot]
-    __shared__ __attribute__((aligned(16))) float pl[4][PD_NC][64];    // attention: probabilities, transposed
-    __shared__ uint16_t hout[RF];
-    __shared__ float bv[4];
-    __shared__ int bi[4];
+    using LY = Lds<Q8>;
+    __shared__ __attribute__((aligned(1024))) char lds[LY::BYTES];
+    f16 *xs = reinterpret_cast<f16 *>(lds + LDS_XS);      // current residual stream
+    f16 *xn = reinterpret_cast<f16 *>(lds + LDS_XN);      // normalized input / attention output
+    float *bv = reinterpret_cast<float *>(lds + LDS_MISC);
+    int *bi = reinterpret_cast<int *>(lds + LDS_MISC + 16);
+    float *sm = reinterpret_cast<float *>(lds + LDS_MISC + 32), *sl = reinterpret_cast<float *>(lds + LDS_MISC + 48);
+    uint16_t *hout = reinterpret_cast<uint16_t *>(lds + LDS_MISC + 64);   // RF values
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wg = blockIdx.x;
     const int token = a.state[0], pos = a.state[1];
@@ -282,257 +348,326 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     };
     mark(63);
     if (a.trace && tid == 0 && wg == 0) a.trace[126] = __builtin_amdgcn_s_memtime();
-    uint64_t *LX = a.ll + LL_X, *LQ = a.ll + LL_QKV, *LA = a.ll + LL_ATT, *LHd = a.ll + LL_HID, *LC = a.ll + LL_CAND;
+    uint64_t *LX = a.ll + LL_X, *LA = a.ll + LL_ATT, *LHd = a.ll + LL_HID, *LC = a.ll + LL_CAND;
     const size_t hstride = (size_t)a.maxT * PD_D;
-
 
     auto read_x = [&](uint32_t flag) {
         return ll_read<3>(LX, PD_E, flag, a.err, a.spin, [](int i) { return i; },
                           [&](int i, uint32_t d) { xs[i] = __builtin_bit_cast(f16, (uint16_t)d); });
     };
 
-    for (int l = 0; l < GPT2_N_LAYER; ++l) {
-        const PDLayer &ly = a.layers[l];
-        const int ph = 5 * l;
-        // ---- Q: LN1 + QKV rows [wg*RQ, +RQ)
-        {
-            const bool q8 = ly.s[0] != nullptr;
-            PhaseW<768, true, RQ> P8;
-            PhaseW<768, false, RQ> P16;
-            if (q8) load_phase(P8, ly.w[0], ly.s[0], ly.b[0], wg * RQ, wave, lane);
-            else load_phase(P16, ly.w[0], nullptr, ly.b[0], wg * RQ, wave, lane);
+    if (wg < PD_NA) {
+        // ================================ attention work-group: head h, key split sp
+        // Per layer: LN1 of x; the head's q and this split's slices of k and v of key `pos`, from
+        // the weight rows staged in LDS during the previous layer; the K/V append of those slices;
+        // attention of q over the split's share of keys [0, pos); then the unnormalized partial
+        // (m, l, c[64]), the slice's share of q.k_pos and the v_pos slice to the exchange.  The
+        // combiner treats key `pos` as one more partial (m = q.k_pos / 8, l = 1, c = v_pos).
+        const int h = wg / PD_S, sp = wg % PD_S;
+        const int per = (pos + PD_S - 1) / PD_S;
+        const int j0 = min(pos, sp * per), j1 = min(pos, j0 + per);
+        const int pw = (j1 - j0 + 3) / 4;                  // keys per wave, <= 64 (maxT <= N_CTX)
+        const int w0 = min(j1, j0 + pw * wave), w1 = min(j1, w0 + pw);
+        const int slot = lane >> 3, dg = (lane & 7) * 8;
+        char *ldw = lds + LY::W;
+        f16 *qkvh = reinterpret_cast<f16 *>(lds + LY::QKVH);
+        float *qs = reinterpret_cast<float *>(lds + LY::QSB), *qb = qs + QR;
+        float(*cl)[PD_D][8] = reinterpret_cast<float(*)[PD_D][8]>(lds + LY::CL);
+        float(*pl)[64] = reinterpret_cast<float(*)[64]>(lds + LY::PL);
+        dma_qkv<LY::RB>(ldw, a.layers[0].w[0], h, sp, wave, lane);
+        for (int l = 0; l < GPT2_N_LAYER; ++l) {
+            const PDLayer &ly = a.layers[l];
+            uint16_t *Kc = a.kv + (size_t)(2 * l) * PD_H * hstride + h * hstride;
+            uint16_t *Vc = a.kv + (size_t)(2 * l + 1) * PD_H * hstride + h * hstride;
+            // ---- before the input arrives: the wave's keys/values, LN1 params, q/k/v scales and biases
+            const f16x8 z8 = {};
+            f16x8 kr[8], vr[8];
+            {
+                const int jk = w0 + lane;
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+                    kr[c] = (jk < w1) ? *reinterpret_cast<const f16x8 *>(Kc + (size_t)jk * PD_D + 8 * c) : z8;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const int key = w0 + slot + 8 * t;
+                    vr[t] = (key < w1) ? *reinterpret_cast<const f16x8 *>(Vc + (size_t)key * PD_D + dg) : z8;
+                }
+            }
             LNParams lnp;
             load_ln(lnp, ly.ln1_g, ly.ln1_b);
+            float rs = 1.f;
+            uint16_t rb = 0;   // fp16 bits
+            if (tid < QR) {
+                const int gr = qkv_row(h, sp, tid);
+                rs = Q8 ? ly.s[0][gr] : 1.f;
+                rb = ly.b[0][gr];
+            }
+            // ---- x: embed (layer 0) or the previous layer's output
             if (l == 0) {
-                // embed: x = fp16(wte[token] + wpe[pos]) (every work-group, no exchange)
 #pragma unroll
                 for (int i = 0; i < 3; ++i) {
                     const int e = tid + PD_T * i;
                     xs[e] = (f16)(h2f(a.wte[(size_t)token * PD_E + e]) + h2f(a.wpe[(size_t)pos * PD_E + e]));
                 }
                 __syncthreads();
-            } else if (!read_x(seq(ph - 1))) {
+            } else if (!read_x(seq(4 * l - 1))) {
                 return;
             }
-            mark(64 + ph);
-            layernorm768(xn, xs, lnp, lane);
-            auto out = [&](int k, float v) {
-                if (lane == 0) ll_st(LQ + wg * RQ + k, __builtin_bit_cast(uint16_t, (f16)v), seq(ph));
-            };
-            if (q8) run_phase(P8, xn, wave, lane, out);
-            else run_phase(P16, xn, wave, lane, out);
-            mark(ph);
-        }
-        // ---- A: attention, head h, key split sp (work-groups 0 .. H*S-1); each wave takes up to
-        // PD_NC chunks of 64 keys.  Keys and values of past positions do not depend on this token,
-        // so each lane loads its key rows and value slices before q arrives; key `pos` comes from the
-        // exchanged qkv.  One softmax pass over the wave's keys (no rescaling between chunks).
-        if (wg < PD_H * PD_S) {
-            const int h = wg / PD_S, sp = wg % PD_S;
-            uint16_t *Kc = a.kv + (size_t)(2 * l) * PD_H * hstride + h * hstride;
-            uint16_t *Vc = a.kv + (size_t)(2 * l + 1) * PD_H * hstride + h * hstride;
-            const int len = pos + 1;
-            const int per = (len + PD_S - 1) / PD_S;
-            const int j0 = min(len, sp * per), j1 = min(len, j0 + per);
-            const int w0 = min(j1, j0 + 64 * PD_NC * wave), w1 = min(j1, w0 + 64 * PD_NC);
-            const int slot = lane >> 3, dg = (lane & 7) * 8;
-            const f16x8 z8 = {};
-            f16x8 kr[PD_NC][8], vr[PD_NC][8];
+            mark(64 + 4 * l);
+            wait_vm<0>();        // this wave's weight DMA has landed (all waves: the barrier below)
+            if (l == 1) mark(113);
+            if (tid < QR) {
+                qs[tid] = rs;
+                qb[tid] = h2f(rb);
+            }
+            layernorm768(xn, xs, lnp, lane);   // ends with a barrier
+            if (l == 1) mark(114);
+            // ---- the QR rows: 16 lanes per row, 4 rows per wave per pass, two passes at a time
+            {
+                constexpr int CPL = LY::RB / 256;          // 16-byte chunks per lane: 3 (int8), 6 (fp16)
+                const int j = lane & 15, rsl = lane >> 4;
+                // x elements of chunk j + 16i: int8 rows 16 per chunk (two f16x8), fp16 rows 8 (one)
+                f16x8 xr[6];
 #pragma unroll
-            for (int ch = 0; ch < PD_NC; ++ch) {
-                const int jk = w0 + 64 * ch + lane;
+                for (int i = 0; i < 6; ++i)
+                    xr[i] = Q8 ? *reinterpret_cast<const f16x8 *>(xn + (j + 16 * (i >> 1)) * 16 + 8 * (i & 1))
+                               : *reinterpret_cast<const f16x8 *>(xn + (j + 16 * i) * 8);
+                auto dot = [&](const uint4(&w)[CPL]) {
+                    float acc = 0.f;
 #pragma unroll
-                for (int c = 0; c < 8; ++c)
-                    kr[ch][c] = (jk < w1 && jk != pos) ? *reinterpret_cast<const f16x8 *>(Kc + (size_t)jk * PD_D + 8 * c) : z8;
+                    for (int i = 0; i < CPL; ++i) {
+                        const uint32_t wd[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
 #pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const int key = w0 + 64 * ch + slot + 8 * t;
-                    vr[ch][t] = (key < w1 && key != pos) ? *reinterpret_cast<const f16x8 *>(Vc + (size_t)key * PD_D + dg) : z8;
+                        for (int t = 0; t < 4; ++t) {
+                            if constexpr (Q8) {
+                                f16x2 lo, hi;
+                                i8x4_to_f16x4_v(wd[t], lo, hi);
+                                const f16x8 &xv = xr[2 * i + (t >> 1)];
+                                const int o = (t & 1) * 4;
+                                acc = __builtin_amdgcn_fdot2(lo, f16x2{xv[o], xv[o + 1]}, acc, false);
+                                acc = __builtin_amdgcn_fdot2(hi, f16x2{xv[o + 2], xv[o + 3]}, acc, false);
+                            } else {
+                                acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, wd[t]),
+                                                             f16x2{xr[i][2 * t], xr[i][2 * t + 1]}, acc, false);
+                            }
+                        }
+                    }
+                    return acc;
+                };
+#pragma unroll
+                for (int p = 0; p < QR / 16; p += 2) {
+                    const int ra = 16 * p + 4 * wave + rsl, rb2 = ra + 16;
+                    uint4 wa[CPL], wb[CPL];
+#pragma unroll
+                    for (int i = 0; i < CPL; ++i) {
+                        wa[i] = *reinterpret_cast<const uint4 *>(ldw + ra * LY::RB + (j + 16 * i) * 16);
+                        wb[i] = *reinterpret_cast<const uint4 *>(ldw + rb2 * LY::RB + (j + 16 * i) * 16);
+                    }
+                    float aa = dot(wa), ab = dot(wb);
+                    aa = row16_sum(aa);
+                    ab = row16_sum(ab);
+                    if (j == 0) {
+                        qkvh[ra] = (f16)(aa * qs[ra] + qb[ra]);
+                        qkvh[rb2] = (f16)(ab * qs[rb2] + qb[rb2]);
+                    }
                 }
             }
-            auto qidx = [h](int i) { return (i >> 6) * PD_E + h * PD_D + (i & 63); };
-            if (!ll_read<1>(LQ, 3 * PD_D, seq(ph), a.err, a.spin, qidx,
-                            [&](int i, uint32_t d) { qkvh[i] = __builtin_bit_cast(f16, (uint16_t)d); }))
-                return;
-            mark(64 + ph + 1);
-            if (sp == 0 && tid < PD_D) {
-                Kc[(size_t)pos * PD_D + tid] = __builtin_bit_cast(uint16_t, qkvh[PD_D + tid]);
-                Vc[(size_t)pos * PD_D + tid] = __builtin_bit_cast(uint16_t, qkvh[2 * PD_D + tid]);
+            lds_barrier();
+            if (l == 1) mark(115);
+            if (tid < KS) {
+                Kc[(size_t)pos * PD_D + KS * sp + tid] = __builtin_bit_cast(uint16_t, qkvh[PD_D + tid]);
+                Vc[(size_t)pos * PD_D + KS * sp + tid] = __builtin_bit_cast(uint16_t, qkvh[PD_D + KS + tid]);
             }
-            // Scores: lane = key of each chunk.  m and l are wave-uniform; the probabilities go to
-            // LDS transposed so that lane (slot, dg) reads the eight it needs (keys slot + 8t) as two
-            // 16-byte loads, and its context slice (8 dims over its 8 keys) goes back to LDS for the
-            // cross-slot, cross-wave merge.
+            // ---- attention over the wave's keys (one softmax pass), then the work-group merge
             float m_w = -INFINITY, l_w = 0.f;
             float cacc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
             if (w0 < w1) {
                 f16x8 q[8];
                 load_q(q, reinterpret_cast<const uint16_t *>(qkvh));
-                float sv[PD_NC], pv[PD_NC];
-                float mloc = -INFINITY;
+                const bool on = w0 + lane < w1;
+                float sv = -INFINITY;
+                if (on) {
+                    float d0 = 0.f, d1 = 0.f;
 #pragma unroll
-                for (int ch = 0; ch < PD_NC; ++ch) {
-                    const int jk = w0 + 64 * ch + lane;
-                    if (jk == pos) load_q(kr[ch], reinterpret_cast<const uint16_t *>(qkvh + PD_D));
-                    sv[ch] = -INFINITY;
-                    if (jk < w1) {
-                        float d0 = 0.f, d1 = 0.f;
+                    for (int c = 0; c < 8; ++c)
 #pragma unroll
-                        for (int c = 0; c < 8; ++c)
-#pragma unroll
-                            for (int t = 0; t < 4; t += 2) {
-                                d0 = __builtin_amdgcn_fdot2(f16x2{q[c][2 * t], q[c][2 * t + 1]},
-                                                            f16x2{kr[ch][c][2 * t], kr[ch][c][2 * t + 1]}, d0, false);
-                                d1 = __builtin_amdgcn_fdot2(f16x2{q[c][2 * t + 2], q[c][2 * t + 3]},
-                                                            f16x2{kr[ch][c][2 * t + 2], kr[ch][c][2 * t + 3]}, d1, false);
-                            }
-                        sv[ch] = (d0 + d1) * 0.125f;
-                    }
-                    mloc = fmaxf(mloc, sv[ch]);
+                        for (int t = 0; t < 4; t += 2) {
+                            d0 = __builtin_amdgcn_fdot2(f16x2{q[c][2 * t], q[c][2 * t + 1]}, f16x2{kr[c][2 * t], kr[c][2 * t + 1]},
+                                                        d0, false);
+                            d1 = __builtin_amdgcn_fdot2(f16x2{q[c][2 * t + 2], q[c][2 * t + 3]},
+                                                        f16x2{kr[c][2 * t + 2], kr[c][2 * t + 3]}, d1, false);
+                        }
+                    sv = (d0 + d1) * 0.125f;
                 }
-                m_w = wave_max_u(mloc);   // finite: key w0 is in range
-                float psum = 0.f;
+                m_w = wave_max_u(sv);   // finite: key w0 is in range
+                const float pv = on ? __expf(sv - m_w) : 0.f;
+                pl[wave][(lane & 7) * 8 + (lane >> 3)] = pv;
+                l_w = wave_sum_u(pv);
+                const float4 pa = *reinterpret_cast<const float4 *>(&pl[wave][slot * 8]);
+                const float4 pb = *reinterpret_cast<const float4 *>(&pl[wave][slot * 8 + 4]);
+                const float pr[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
 #pragma unroll
-                for (int ch = 0; ch < PD_NC; ++ch) {
-                    pv[ch] = (w0 + 64 * ch + lane < w1) ? __expf(sv[ch] - m_w) : 0.f;
-                    psum += pv[ch];
-                    pl[wave][ch][(lane & 7) * 8 + (lane >> 3)] = pv[ch];
-                }
-                l_w = wave_sum_u(psum);
+                for (int t = 0; t < 8; ++t)
 #pragma unroll
-                for (int ch = 0; ch < PD_NC; ++ch) {
-                    const float4 pa = *reinterpret_cast<const float4 *>(&pl[wave][ch][slot * 8]);
-                    const float4 pb = *reinterpret_cast<const float4 *>(&pl[wave][ch][slot * 8 + 4]);
-                    const float pr[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) {
-                        const int key = w0 + 64 * ch + slot + 8 * t;
-                        const f16x8 vv = (key == pos) ? *reinterpret_cast<const f16x8 *>(qkvh + 2 * PD_D + dg) : vr[ch][t];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) cacc[e] += pr[t] * (float)vv[e];   // p = 0 past w1
-                    }
-                }
+                    for (int e = 0; e < 8; ++e) cacc[e] += pr[t] * (float)vr[t][e];   // p = 0 past w1
             }
-            // context slices to LDS: cl[wave][dim][slot]
 #pragma unroll
             for (int e = 0; e < 8; ++e) cl[wave][dg + e][slot] = cacc[e];
             if (lane == 0) {
                 sm[wave] = m_w;
                 sl[wave] = l_w;
             }
-            __syncthreads();
-            // unnormalized partial over the work-group's keys: m, l, c[64]
+            if (l == 1) mark(116);
+            lds_barrier();
+            if (l == 1) mark(117);
             if (tid < PD_PW) {
-                float mx = -INFINITY;
+                float val = 0.f;
+                if (tid < 2 + PD_D) {
+                    // the four waves' partials merged, branch-free (independent LDS reads)
+                    float mw[4], lw[4], fw[4];
 #pragma unroll
-                for (int w = 0; w < 4; ++w)
-                    if (sl[w] != 0.f) mx = fmaxf(mx, sm[w]);
-                float val = (tid == 0) ? mx : 0.f;
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    if (sl[w] == 0.f) continue;
-                    const float f = __expf(sm[w] - mx);
-                    if (tid == 1) val += sl[w] * f;
-                    if (tid >= 2) {
-                        const float4 ca = *reinterpret_cast<const float4 *>(&cl[w][tid - 2][0]);
-                        const float4 cb = *reinterpret_cast<const float4 *>(&cl[w][tid - 2][4]);
-                        val += (((ca.x + ca.y) + (ca.z + ca.w)) + ((cb.x + cb.y) + (cb.z + cb.w))) * f;
+                    for (int w = 0; w < 4; ++w) {
+                        mw[w] = sm[w];
+                        lw[w] = sl[w];
                     }
+                    float mx = -INFINITY;
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) mx = (lw[w] != 0.f) ? fmaxf(mx, mw[w]) : mx;
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) fw[w] = (lw[w] != 0.f) ? __expf(mw[w] - mx) : 0.f;
+                    if (tid == 0) {
+                        val = mx;
+                    } else if (tid == 1) {
+#pragma unroll
+                        for (int w = 0; w < 4; ++w) val += lw[w] * fw[w];
+                    } else {
+#pragma unroll
+                        for (int w = 0; w < 4; ++w) {
+                            const float4 ca = *reinterpret_cast<const float4 *>(&cl[w][tid - 2][0]);
+                            const float4 cb = *reinterpret_cast<const float4 *>(&cl[w][tid - 2][4]);
+                            val += (((ca.x + ca.y) + (ca.z + ca.w)) + ((cb.x + cb.y) + (cb.z + cb.w))) * fw[w];
+                        }
+                    }
+                } else if (tid == 2 + PD_D) {
+                    // q[KS*sp ..] . k_pos[KS*sp ..] in fp32 from the fp16 values
+#pragma unroll
+                    for (int i = 0; i < KS; ++i) val += (float)qkvh[KS * sp + i] * (float)qkvh[PD_D + i];
+                } else {
+                    val = (float)qkvh[PD_D + KS + (tid - 3 - PD_D)];
                 }
-                ll_st(LA + (h * PD_S + sp) * PD_PW + tid, __float_as_uint(val), seq(ph + 1));
+                ll_st(LA + wg * PD_PW + tid, __float_as_uint(val), seq(4 * l));
             }
-            __syncthreads();
-            mark(ph + 1);
+            if (l == 1) mark(118);
+            lds_barrier();   // the attention scratch (aliasing the weights) is free again
+            mark(4 * l);
+            if (l + 1 < GPT2_N_LAYER) dma_qkv<LY::RB>(ldw, a.layers[l + 1].w[0], h, sp, wave, lane);
         }
-        // ---- P: combine heads, proj rows [wg*RP, +RP), + bias + residual
-        {
-            const bool q8 = ly.s[1] != nullptr;
-            PhaseW<768, true, RP> P8;
-            PhaseW<768, false, RP> P16;
-            if (q8) load_phase(P8, ly.w[1], ly.s[1], ly.b[1], wg * RP, wave, lane);
-            else load_phase(P16, ly.w[1], nullptr, ly.b[1], wg * RP, wave, lane);
-            constexpr int NA = PD_H * PD_S * PD_PW;
-            if (!ll_read<(NA + PD_T - 1) / PD_T>(LA, NA, seq(ph + 1), a.err, a.spin, [](int i) { return i; },
+    } else if (wg - PD_NA < PD_NW) {
+        // ================================ GEMV work-group g: proj, fc and mlp-proj rows
+        // A work-group polls a buffer only in a phase it writes from, so every writer of the next
+        // version of a buffer has first read everything its readers needed.  Each phase's weight
+        // rows are loaded while the phase before it runs (after that phase's input has arrived, so
+        // the polls never queue behind weight loads).
+        const int g = wg - PD_NA;
+        f16 *hs = reinterpret_cast<f16 *>(lds + LY::HS);
+        float *part = reinterpret_cast<float *>(lds + LY::PART);
+        // Residual rows [g*RP, +RP) of x after the previous layer: this work-group wrote them itself
+        // (its mlp-proj rows), layer 0 starts from the embedding.
+        float xown[RP];
+#pragma unroll
+        for (int k = 0; k < RP; ++k) {
+            const int r = g * RP + k;
+            xown[k] = (float)(f16)(h2f(a.wte[(size_t)token * PD_E + r]) + h2f(a.wpe[(size_t)pos * PD_E + r]));
+        }
+        PhaseW<768, Q8, RP> WP;
+        PhaseW<768, Q8, RF> WF;
+        PhaseW<3072, Q8, RM> WM;
+        load_phase(WP, a.layers[0].w[1], a.layers[0].s[1], a.layers[0].b[1], g * RP, wave, lane);
+        for (int l = 0; l < GPT2_N_LAYER; ++l) {
+            const PDLayer &ly = a.layers[l];
+            // ---- P: combine the attention words, proj rows, + bias + residual
+            constexpr int NA = PD_NA * PD_PW;
+            if (!ll_read<(NA + PD_T - 1) / PD_T>(LA, NA, seq(4 * l), a.err, a.spin, [](int i) { return i; },
                                                  [&](int i, uint32_t d) { part[i] = __uint_as_float(d); }))
                 return;
-            mark(64 + ph + 2);
+            mark(64 + 4 * l + 1);
+            load_phase(WF, ly.w[2], ly.s[2], ly.b[2], g * RF, wave, lane);
+            LNParams lnp;
+            load_ln(lnp, ly.ln2_g, ly.ln2_b);
+            // Element e = tid + 256i: wave w handles head w + 4i, so the per-head weights are
+            // wave-uniform; every lane computes them (broadcast LDS reads, no branches).
+            static_assert(PD_S == 4 && PD_T / PD_D == 4, "four slices per head, one head per wave and element");
 #pragma unroll
             for (int i = 0; i < 3; ++i) {
-                const int e = tid + PD_T * i, h = e / PD_D, d = e % PD_D;
-                float mx = -INFINITY;
+                const int e = tid + PD_T * i, hh = e / PD_D, d = e % PD_D;
+                const float *p = part + hh * PD_S * PD_PW;
+                float m4[PD_S], l4[PD_S], s4[PD_S], f4[PD_S], c4[PD_S];
 #pragma unroll
-                for (int s = 0; s < PD_S; ++s) {
-                    const float *p = part + (h * PD_S + s) * PD_PW;
-                    if (p[1] != 0.f) mx = fmaxf(mx, p[0]);
+                for (int s2 = 0; s2 < PD_S; ++s2) {
+                    m4[s2] = p[s2 * PD_PW];
+                    l4[s2] = p[s2 * PD_PW + 1];
+                    s4[s2] = p[s2 * PD_PW + 2 + PD_D];
+                    c4[s2] = p[s2 * PD_PW + 2 + d];
                 }
-                float L = 0.f, c = 0.f;
+                const float vpos = p[(d / KS) * PD_PW + 3 + PD_D + d % KS];
+                // key `pos`: m = q.k_pos / 8 from the four slices' parts, l = 1, c = v_pos
+                const float spos = ((s4[0] + s4[1]) + (s4[2] + s4[3])) * 0.125f;
+                float mx = spos;
 #pragma unroll
-                for (int s = 0; s < PD_S; ++s) {
-                    const float *p = part + (h * PD_S + s) * PD_PW;
-                    if (p[1] == 0.f) continue;
-                    const float f = __expf(p[0] - mx);
-                    L += p[1] * f;
-                    c += p[2 + d] * f;
+                for (int s2 = 0; s2 < PD_S; ++s2) mx = (l4[s2] != 0.f) ? fmaxf(mx, m4[s2]) : mx;
+#pragma unroll
+                for (int s2 = 0; s2 < PD_S; ++s2) f4[s2] = (l4[s2] != 0.f) ? __expf(m4[s2] - mx) : 0.f;
+                float L = __expf(spos - mx);
+                float c = L * vpos;
+#pragma unroll
+                for (int s2 = 0; s2 < PD_S; ++s2) {
+                    L += l4[s2] * f4[s2];
+                    c += c4[s2] * f4[s2];
                 }
                 xn[e] = (f16)(c / L);
             }
-            __syncthreads();
-            auto out = [&](int k, float v) {
-                const int r = wg * RP + k;
-                if (lane == 0) ll_st(LX + r, __builtin_bit_cast(uint16_t, (f16)(v + (float)xs[r])), seq(ph + 2));
-            };
-            if (q8) run_phase(P8, xn, wave, lane, out);
-            else run_phase(P16, xn, wave, lane, out);
-            mark(ph + 2);
-        }
-        // ---- F: LN2 + fc rows [wg*RF, +RF) + gelu, exchanged in pairs
-        {
-            const bool q8 = ly.s[2] != nullptr;
-            PhaseW<768, true, RF> P8;
-            PhaseW<768, false, RF> P16;
-            if (q8) load_phase(P8, ly.w[2], ly.s[2], ly.b[2], wg * RF, wave, lane);
-            else load_phase(P16, ly.w[2], nullptr, ly.b[2], wg * RF, wave, lane);
-            LNParams lnp;
-            load_ln(lnp, ly.ln2_g, ly.ln2_b);
-            if (!read_x(seq(ph + 2))) return;
-            mark(64 + ph + 3);
+            if (l == 1) mark(118);
+            lds_barrier();
+            if (l == 1) mark(119);
+            run_phase(WP, xn, wave, lane, [&](int k, float v) {
+                if (lane == 0) ll_st(LX + g * RP + k, __builtin_bit_cast(uint16_t, (f16)(v + xown[k])), seq(4 * l + 1));
+            });
+            mark(4 * l + 1);
+            // ---- F: LN2 + fc rows [g*RF, +RF) + gelu, exchanged in pairs
+            if (!read_x(seq(4 * l + 1))) return;
+            mark(64 + 4 * l + 2);
+            load_phase(WM, ly.w[3], ly.s[3], ly.b[3], g * RM, wave, lane);
             layernorm768(xn, xs, lnp, lane);
-            auto out = [&](int k, float v) {
+            if (l == 1) mark(120);
+            run_phase(WF, xn, wave, lane, [&](int k, float v) {
                 if (lane == 0) hout[k] = __builtin_bit_cast(uint16_t, (f16)gelu_tanh(v));
-            };
-            if (q8) run_phase(P8, xn, wave, lane, out);
-            else run_phase(P16, xn, wave, lane, out);
-            __syncthreads();
+            });
+            if (l == 1) mark(121);
+            lds_barrier();
             if (tid < RF / 2)
-                ll_st(LHd + wg * (RF / 2) + tid, (uint32_t)hout[2 * tid] | ((uint32_t)hout[2 * tid + 1] << 16), seq(ph + 3));
-            mark(ph + 3);
-        }
-        // ---- M: mlp-proj rows [wg*RM, +RM) over gelu(fc), + bias + residual
-        {
-            const bool q8 = ly.s[3] != nullptr;
-            PhaseW<3072, true, RM> P8;
-            PhaseW<3072, false, RM> P16;
-            if (q8) load_phase(P8, ly.w[3], ly.s[3], ly.b[3], wg * RM, wave, lane);
-            else load_phase(P16, ly.w[3], nullptr, ly.b[3], wg * RM, wave, lane);
-            if (!ll_read<PD_F / 2 / PD_T>(LHd, PD_F / 2, seq(ph + 3), a.err, a.spin, [](int i) { return i; },
+                ll_st(LHd + g * RF / 2 + tid, (uint32_t)hout[2 * tid] | ((uint32_t)hout[2 * tid + 1] << 16), seq(4 * l + 2));
+            mark(4 * l + 2);
+            // ---- M: mlp-proj rows [g*RM, +RM) over gelu(fc), + bias + residual
+            if (!ll_read<PD_F / 2 / PD_T>(LHd, PD_F / 2, seq(4 * l + 2), a.err, a.spin, [](int i) { return i; },
                                           [&](int i, uint32_t d) {
                                               hs[2 * i] = __builtin_bit_cast(f16, (uint16_t)(d & 0xffff));
                                               hs[2 * i + 1] = __builtin_bit_cast(f16, (uint16_t)(d >> 16));
                                           }))
                 return;
-            mark(64 + ph + 4);
-            auto out = [&](int k, float v) {
-                const int r = wg * RM + k;
-                if (lane == 0) ll_st(LX + r, __builtin_bit_cast(uint16_t, (f16)(v + (float)xs[r])), seq(ph + 4));
-            };
-            if (q8) run_phase(P8, hs, wave, lane, out);
-            else run_phase(P16, hs, wave, lane, out);
-            mark(ph + 4);
+            mark(64 + 4 * l + 3);
+            if (l + 1 < GPT2_N_LAYER)
+                load_phase(WP, a.layers[l + 1].w[1], a.layers[l + 1].s[1], a.layers[l + 1].b[1], g * RP, wave, lane);
+            run_phase(WM, hs, wave, lane, [&](int k, float v) {
+                const int r = g * RM + k;
+                const f16 o = (f16)(v + (float)xs[r]);
+                xown[k] = (float)o;
+                if (lane == 0) ll_st(LX + r, __builtin_bit_cast(uint16_t, o), seq(4 * l + 3));
+            });
+            mark(4 * l + 3);
         }
     }
-
     // ---- head: LN_f, logits rows [wg*RH, ...), local argmax, then work-group 0 picks the token
-    const int ph = 5 * GPT2_N_LAYER;
+    const int ph = PH_CAND;
     LNParams lnf;
     load_ln(lnf, a.lnf_g, a.lnf_b);
     if (!read_x(seq(ph - 1))) return;
@@ -544,20 +679,20 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     // 16-byte chunks j, j+16, ...; HD passes of loads in flight per wave (the persistent step has only
     // four waves per CU, so the memory parallelism comes from inside the wave).
     auto head_rows = [&](auto q8tag) {
-        constexpr bool Q8 = decltype(q8tag)::value;
-        constexpr int CPL = Q8 ? 3 : 6, HD = 4;
+        constexpr bool HQ = decltype(q8tag)::value;
+        constexpr int CPL = HQ ? 3 : 6, HD = 4;
         const int j = lane & 15, slot = lane >> 4;
-        f16x8 xr[Q8 ? 2 * CPL : CPL];
+        f16x8 xr[HQ ? 2 * CPL : CPL];
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
-            if constexpr (Q8) {
+            if constexpr (HQ) {
                 xr[2 * i] = *reinterpret_cast<const f16x8 *>(xn + (j + 16 * i) * 16);
                 xr[2 * i + 1] = *reinterpret_cast<const f16x8 *>(xn + (j + 16 * i) * 16 + 8);
             } else {
                 xr[i] = *reinterpret_cast<const f16x8 *>(xn + (j + 16 * i) * 8);
             }
         }
-        constexpr int ROWB = Q8 ? PD_E : 2 * PD_E;
+        constexpr int ROWB = HQ ? PD_E : 2 * PD_E;
         const char *W = reinterpret_cast<const char *>(a.head_w);
         uint4 ring[HD][CPL];
         auto issue = [&](uint4(&buf)[CPL], int pass) {
@@ -573,7 +708,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
 #pragma unroll
             for (int i = 0; i < CPL; ++i) {
                 const uint32_t wd[4] = {buf[i].x, buf[i].y, buf[i].z, buf[i].w};
-                if constexpr (Q8) {
+                if constexpr (HQ) {
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
                         f16x2 lo, hi;
@@ -593,7 +728,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             acc = row16_sum(acc);
             if (r < r1) {
                 float v = acc;
-                if constexpr (Q8) v *= a.head_s[r];
+                if constexpr (HQ) v *= a.head_s[r];
                 const uint16_t hv = __builtin_bit_cast(uint16_t, (f16)v);
                 if (j == 0) a.logits[r] = hv;
                 const float fv = h2f(hv);
@@ -637,7 +772,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     }
     if (wg != 0) return;
     // work-group 0: argmax over the candidates, advance the state
-    __shared__ uint32_t cands[PD_G];
+    uint32_t *cands = reinterpret_cast<uint32_t *>(lds + LY::CANDS);
     if (!ll_read<(PD_G + PD_T - 1) / PD_T>(LC, PD_G, seq(ph), a.err, a.spin, [](int i) { return i; },
                                           [&](int i, uint32_t d) { cands[i] = d; }))
         return;
@@ -684,7 +819,8 @@ bool persist_plan(PDPlan &p, const GPT2Backend *be, const GPT2WeightsGPU *w, GPT
     if (be->gemv != gpt2_gemv_fp16) return false;
     const bool q_ok = be->gemv_q == gpt2_gemv_int8;
     const GPT2QWeightsGPU *qw = w->q;
-    PDLayer h[GPT2_N_LAYER];
+    PDArgs &a = p.args;
+    PDLayer *h = a.layers;
     for (int L = 0; L < GPT2_N_LAYER; ++L) {
         const GPT2LayerGPU &g = w->layers[L];
         const GPT2QLayerGPU *ql = qw ? &qw->layers[L] : nullptr;
@@ -701,12 +837,16 @@ bool persist_plan(PDPlan &p, const GPT2Backend *be, const GPT2WeightsGPU *w, GPT
             h[L].w[i] = q ? (const void *)wq[i]->q : (const void *)wh[i];
             h[L].s[i] = q ? wq[i]->s : nullptr;
             h[L].b[i] = bh[i];
+            if (!bh[i]) return false;   // the step loads every bias unconditionally
         }
     }
-    p.d_layers = (PDLayer *)gpt2_dmalloc(sizeof(h));
-    if (!p.d_layers || gpt2_h2d(p.d_layers, h, sizeof(h))) return false;
-    PDArgs &a = p.args;
-    a.layers = p.d_layers;
+    // one kernel instance per weight kind: every layer matrix int8, or every one fp16
+    int nq = 0;
+    for (int L = 0; L < GPT2_N_LAYER; ++L)
+        for (int i = 0; i < 4; ++i) nq += h[L].s[i] != nullptr;
+    if (nq != 0 && nq != 4 * GPT2_N_LAYER) return false;
+    if (kv->maxT > GPT2_N_CTX) return false;   // an attention wave holds at most 64 keys
+    p.q8 = nq != 0;
     a.wte = w->wte;
     a.wpe = w->wpe;
     a.lnf_g = w->lnf_g;
@@ -727,7 +867,8 @@ bool persist_plan(PDPlan &p, const GPT2Backend *be, const GPT2WeightsGPU *w, GPT
 }
 
 void persist_launch(const PDPlan &p, hipStream_t s) {
-    hipLaunchKernelGGL(k_decode_persist, dim3(PD_G), dim3(PD_T), 0, s, p.args);
+    if (p.q8) hipLaunchKernelGGL(k_decode_persist<true>, dim3(PD_G), dim3(PD_T), 0, s, p.args);
+    else hipLaunchKernelGGL(k_decode_persist<false>, dim3(PD_G), dim3(PD_T), 0, s, p.args);
 }
 
 size_t persist_ll_bytes() { return (size_t)LL_WORDS * 8; }
@@ -739,17 +880,11 @@ size_t persist_ll_bytes() { return (size_t)LL_WORDS * 8; }
 // forces the timeout path with every kernel still exiting normally.
 extern "C" void gpt2_tune_decode_spin(int rounds) { g2::g_pd_spin = rounds >= 0 ? rounds : g2::PD_SPIN; }
 // Profiling hook: graphs created afterwards record, per work-group, the end time of every phase of
-// the persistent step (s_memrealtime, 100 MHz) into trace[wg * 64 + phase]: 5*l + {0 qkv, 1 attention,
-// 2 proj, 3 fc, 4 mlp-proj}, 60 head start, 61 head end, 62 step end, 63 step start, and at 64 + p
-// the time phase p's input had arrived; work-group 0 also stores the shader clock counter at step
-// start and end in entries 126 / 127.  The buffer holds 256 * 128 entries; nullptr disables.
+// the persistent step (s_memrealtime, 100 MHz) into trace[wg * 128 + phase]: 4*l + {0 LN1 + q/k/v +
+// attention, 1 proj, 2 fc, 3 mlp-proj}, 60 head start, 61 head end, 62 step end, 63 step start, and
+// at 64 + p the time phase p's input had arrived; work-group 0 also stores the shader clock counter at step
+// start and end in entries 126 / 127.  In layer 1 the attention work-groups also record 113 weights
+// landed, 114 LN1 done, 115 q/k/v done, 116 attention done (wave 0), 117 waves merged, 118 words
+// stored; the GEMV work-groups 118 attention combined, 119 past the barrier, 120 LN2 done, 121 fc
+// rows done.  The buffer holds 256 * 128 entries; nullptr disables.
 extern "C" void gpt2_tune_decode_trace(unsigned long long *trace) { g2::g_pd_trace = trace; }
-
-namespace g2 {
-
-void persist_free(PDPlan &p) {
-    gpt2_dfree(p.d_layers);
-    p.d_layers = nullptr;
-}
-
-}  // namespace g2

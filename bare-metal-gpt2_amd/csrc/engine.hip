@@ -381,7 +381,6 @@ struct GPT2DecodeGraph {
 
 static void graph_free(GPT2DecodeGraph *g) {
     if (g->stream) hipStreamDestroy(g->stream);
-    if (g->mode == GPT2_DECODE_PERSISTENT) persist_free(g->plan);
     gpt2_dfree(g->ll);
     gpt2_dfree(g->state);
     delete g;
@@ -416,7 +415,6 @@ extern "C" GPT2DecodeGraph *gpt2_decode_graph_create_mode(const GPT2Backend *be,
             persist_plan(g->plan, be, w, kv, logits, g->state, tokens, g->ll, g->state + 3))
             g->mode = GPT2_DECODE_PERSISTENT;
         else {
-            persist_free(g->plan);
             gpt2_dfree(g->ll);
             g->ll = nullptr;
             gpt2_last_error();   // fall back quietly to the multi-kernel step

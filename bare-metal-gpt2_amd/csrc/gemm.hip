@@ -264,13 +264,6 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(uint16_t *__restrict__ C, con
 //   * INT8 weights stay int8 in LDS (half the bytes) and are widened to exact fp16 as fragments
 //     are read;
 //   * one barrier per k-tile: the buffer refilled at step kt was last read at step kt-1.
-// s_waitcnt immediate for "at most n vector-memory operations outstanding" (gfx9 encoding, expcnt
-// and lgkmcnt left unconstrained).
-template <int n>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(n >= 0 && n < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
-}
 
 // Wait until at most `after` k-tiles of this wave's loads (L instructions each) are outstanding.
 template <int L, int MAXA>
@@ -289,12 +282,7 @@ __device__ __forceinline__ f16x8 i8x8_to_f16x8(uint2 w) {
     return __builtin_bit_cast(f16x8, v);
 }
 
-#define G2_LDS(p) ((__attribute__((address_space(3))) void *)(p))
 
-// Work-group barrier for the LDS ring: the caller has already waited (vmcnt) for its own loads of
-// the tile about to be read; the LDS reads of the previous tile completed before their MFMAs.  The
-// "memory" clobber keeps the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 template <int BN, int BM, int WN, int WM, int S, bool QW>
 __global__ __launch_bounds__(WN *WM * 64) void k_gemm_dl(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
