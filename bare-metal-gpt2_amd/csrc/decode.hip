@@ -65,6 +65,7 @@ constexpr int PD_PW = 2 + PD_D + 1 + KS;           // words it sends: m, l, c[64
 constexpr int RP = 4, RF = 16, RM = 4;             // rows per GEMV work-group: proj, fc, mlp-proj
 constexpr int PD_NW = PD_E / RP;                   // GEMV work-groups with rows (the rest wait for the head)
 constexpr int RH = (PD_V + PD_G - 1) / PD_G;       // head rows per work-group (the last has fewer)
+constexpr int XR = PD_E / PD_T;                    // words of x each thread polls
 static_assert(PD_E % RP == 0 && PD_F % RF == 0 && PD_E / RP == PD_F / RF && RM == RP && PD_NW <= PD_NG,
               "the same GEMV work-groups hold proj, fc and mlp-proj rows");
 static_assert(RF % 2 == 0, "fc rows are exchanged in pairs");
@@ -110,24 +111,28 @@ __device__ __forceinline__ void ll_st(uint64_t *p, uint32_t data, uint32_t flag)
     __hip_atomic_store(p, ((uint64_t)flag << 32) | data, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Polls words idx(i), i in [0, n), of `base` (R per thread, all loads in flight before any check)
+// Polls words [0, n) of `base` (R per thread, word tid + 256r; all loads in flight before any check)
 // until every flag equals `flag`, then calls sink(i, data).  Returns false (for the whole
 // work-group) if a word did not arrive within `spin` rounds or another work-group reported an
-// error; the caller then leaves.
-template <int R, class Idx, class Sink>
-__device__ bool ll_read(const uint64_t *base, int n, uint32_t flag, int *err, int spin, Idx idx, Sink sink) {
+// error; the caller then leaves.  wflag: 4 ints of LDS for the work-group's verdict; dbg (optional,
+// profiling): thread 0 stores the start time and the number of extra poll rounds there.
+static_assert(PD_T == 256, "ll_read combines four waves");
+template <int R, class Sink>
+__device__ bool ll_read(const uint64_t *base, int n, uint32_t flag, int *err, int spin, int *wflag, Sink sink,
+                        unsigned long long *dbg = nullptr) {
+    if (dbg && threadIdx.x == 0) dbg[0] = __builtin_amdgcn_s_memrealtime();
     uint64_t v[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int i = threadIdx.x + PD_T * r;
-        v[r] = (i < n) ? ll_ld(base + idx(i)) : ((uint64_t)flag << 32);
-    }
+    for (int r = 0; r < R; ++r) v[r] = ll_ld(base + min((int)threadIdx.x + PD_T * r, n - 1));
     bool bad = false;
     for (int round = 0;; ++round) {
         bool ok = true;
 #pragma unroll
-        for (int r = 0; r < R; ++r) ok &= (uint32_t)(v[r] >> 32) == flag;
-        if (ok) break;
+        for (int r = 0; r < R; ++r) ok &= (int)threadIdx.x + PD_T * r >= n || (uint32_t)(v[r] >> 32) == flag;
+        if (__all(ok)) {
+            if (dbg && threadIdx.x == 0) dbg[1] = round;
+            break;
+        }
         if (round >= spin || ((round & 63) == 63 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
             bad = true;
             break;
@@ -136,10 +141,15 @@ __device__ bool ll_read(const uint64_t *base, int n, uint32_t flag, int *err, in
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int i = threadIdx.x + PD_T * r;
-            if (i < n && (uint32_t)(v[r] >> 32) != flag) v[r] = ll_ld(base + idx(i));
+            if (i < n && (uint32_t)(v[r] >> 32) != flag) v[r] = ll_ld(base + i);
         }
     }
-    if (__syncthreads_or(bad)) {
+    // The loop is wave-uniform, so `bad` is too.  Barriers here wait for LDS traffic only, so they
+    // do not drain loads issued before the poll.
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) wflag[wave] = bad;
+    lds_barrier();
+    if (wflag[0] | wflag[1] | wflag[2] | wflag[3]) {
         if (threadIdx.x == 0) atomicOr(err, 1);
         return false;
     }
@@ -148,7 +158,7 @@ __device__ bool ll_read(const uint64_t *base, int n, uint32_t flag, int *err, in
         const int i = threadIdx.x + PD_T * r;
         if (i < n) sink(i, (uint32_t)v[r]);
     }
-    __syncthreads();
+    lds_barrier();
     return true;
 }
 
@@ -337,6 +347,8 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     int *bi = reinterpret_cast<int *>(lds + LDS_MISC + 16);
     float *sm = reinterpret_cast<float *>(lds + LDS_MISC + 32), *sl = reinterpret_cast<float *>(lds + LDS_MISC + 48);
     uint16_t *hout = reinterpret_cast<uint16_t *>(lds + LDS_MISC + 64);   // RF values
+    int *wflag = reinterpret_cast<int *>(lds + LDS_MISC + 96);             // ll_read verdicts, 4 ints
+    static_assert(64 + 2 * RF <= 96, "LDS misc layout");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wg = blockIdx.x;
     const int token = a.state[0], pos = a.state[1];
@@ -351,9 +363,9 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     uint64_t *LX = a.ll + LL_X, *LA = a.ll + LL_ATT, *LHd = a.ll + LL_HID, *LC = a.ll + LL_CAND;
     const size_t hstride = (size_t)a.maxT * PD_D;
 
-    auto read_x = [&](uint32_t flag) {
-        return ll_read<3>(LX, PD_E, flag, a.err, a.spin, [](int i) { return i; },
-                          [&](int i, uint32_t d) { xs[i] = __builtin_bit_cast(f16, (uint16_t)d); });
+    auto read_x = [&](uint32_t flag, unsigned long long *dbg = nullptr) {
+        return ll_read<XR>(LX, PD_E, flag, a.err, a.spin, wflag,
+                          [&](int i, uint32_t d) { xs[i] = __builtin_bit_cast(f16, (uint16_t)d); }, dbg);
     };
 
     if (wg < PD_NA) {
@@ -410,11 +422,14 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                     xs[e] = (f16)(h2f(a.wte[(size_t)token * PD_E + e]) + h2f(a.wpe[(size_t)pos * PD_E + e]));
                 }
                 __syncthreads();
-            } else if (!read_x(seq(4 * l - 1))) {
+            } else if (!read_x(seq(4 * l - 1), (l == 1 && a.trace) ? a.trace + wg * 128 + 122 : nullptr)) {
                 return;
             }
             mark(64 + 4 * l);
-            wait_vm<0>();        // this wave's weight DMA has landed (all waves: the barrier below)
+            // This wave's weight DMA has landed (all waves: the barrier below).  It was issued before
+            // everything since, so all but the last XR operations is enough: those are the poll
+            // round of x still in flight, which need not be waited for.
+            wait_vm<XR>();
             if (l == 1) mark(113);
             if (tid < QR) {
                 qs[tid] = rs;
@@ -587,7 +602,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             const PDLayer &ly = a.layers[l];
             // ---- P: combine the attention words, proj rows, + bias + residual
             constexpr int NA = PD_NA * PD_PW;
-            if (!ll_read<(NA + PD_T - 1) / PD_T>(LA, NA, seq(4 * l), a.err, a.spin, [](int i) { return i; },
+            if (!ll_read<(NA + PD_T - 1) / PD_T>(LA, NA, seq(4 * l), a.err, a.spin, wflag,
                                                  [&](int i, uint32_t d) { part[i] = __uint_as_float(d); }))
                 return;
             mark(64 + 4 * l + 1);
@@ -648,7 +663,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 ll_st(LHd + g * RF / 2 + tid, (uint32_t)hout[2 * tid] | ((uint32_t)hout[2 * tid + 1] << 16), seq(4 * l + 2));
             mark(4 * l + 2);
             // ---- M: mlp-proj rows [g*RM, +RM) over gelu(fc), + bias + residual
-            if (!ll_read<PD_F / 2 / PD_T>(LHd, PD_F / 2, seq(4 * l + 2), a.err, a.spin, [](int i) { return i; },
+            if (!ll_read<PD_F / 2 / PD_T>(LHd, PD_F / 2, seq(4 * l + 2), a.err, a.spin, wflag,
                                           [&](int i, uint32_t d) {
                                               hs[2 * i] = __builtin_bit_cast(f16, (uint16_t)(d & 0xffff));
                                               hs[2 * i + 1] = __builtin_bit_cast(f16, (uint16_t)(d >> 16));
@@ -773,7 +788,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     if (wg != 0) return;
     // work-group 0: argmax over the candidates, advance the state
     uint32_t *cands = reinterpret_cast<uint32_t *>(lds + LY::CANDS);
-    if (!ll_read<(PD_G + PD_T - 1) / PD_T>(LC, PD_G, seq(ph), a.err, a.spin, [](int i) { return i; },
+    if (!ll_read<(PD_G + PD_T - 1) / PD_T>(LC, PD_G, seq(ph), a.err, a.spin, wflag,
                                           [&](int i, uint32_t d) { cands[i] = d; }))
         return;
     {
@@ -885,6 +900,6 @@ extern "C" void gpt2_tune_decode_spin(int rounds) { g2::g_pd_spin = rounds >= 0 
 // at 64 + p the time phase p's input had arrived; work-group 0 also stores the shader clock counter at step
 // start and end in entries 126 / 127.  In layer 1 the attention work-groups also record 113 weights
 // landed, 114 LN1 done, 115 q/k/v done, 116 attention done (wave 0), 117 waves merged, 118 words
-// stored; the GEMV work-groups 118 attention combined, 119 past the barrier, 120 LN2 done, 121 fc
-// rows done.  The buffer holds 256 * 128 entries; nullptr disables.
+// stored, 122 start of the poll for x, 123 the number of poll rounds it took beyond the first; the
+// GEMV work-groups 118 attention combined, 119 past the barrier, 120 LN2 done, 121 fc rows done.  The buffer holds 256 * 128 entries; nullptr disables.
 extern "C" void gpt2_tune_decode_trace(unsigned long long *trace) { g2::g_pd_trace = trace; }
