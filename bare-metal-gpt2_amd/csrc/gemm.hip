@@ -282,8 +282,6 @@ __device__ __forceinline__ f16x8 i8x8_to_f16x8(uint2 w) {
     return __builtin_bit_cast(f16x8, v);
 }
 
-
-
 template <int BN, int BM, int WN, int WM, int S, bool QW>
 __global__ __launch_bounds__(WN *WM * 64) void k_gemm_dl(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
                                                          const void *__restrict__ Wv, const float *__restrict__ Ws,

@@ -9,8 +9,9 @@ resident in HBM before the timed region; timing is hipEvents on the launch strea
 Also reported in the same JSON line:
   roofline      the GEMM kernel with the largest share of the step, against 2500 TFLOP/s fp16 MFMA
   gemv_int8     INT8 decode GEMV GB/s per trunk shape, cold (rotating > 512 MB of weight copies,
-                so every launch streams from HBM) and warm (same weights every launch), plus the
-                48-GEMV trunk chain of one decode step
+                so every launch streams from HBM) and warm (same weights every launch), the
+                48-GEMV trunk chain of one decode step, and the same kernel on the INT8 tied head
+                (38.6 MB per launch, where the launch floor no longer hides the streaming rate)
   head_gemv     fp16 tied-head GEMV (77.3 MB) cold / warm
   decode        GPT-2-124M decode tok/s @ctx=512: INT8 trunk + fp16 head, one hipGraph replay per
                 token, after a P=512 prefill; plus the mean over the 511-step greedy run
@@ -204,6 +205,26 @@ def bench_gemv(B):
     ms_chain, _ = B.run_ops(chain, 20, 200)
     res["trunk_chain_48"] = {"bytes": chain_bytes, "us": round(ms_chain * 1e3, 2),
                              "GBs": round(chain_bytes / (ms_chain * 1e-3) / 1e9, 1)}
+    # the same kernel on the INT8 tied head (38.6 MB, no bias): large enough that the launch floor
+    # no longer hides the streaming rate
+    N, K = VOCAB, 768
+    w16 = B.dev(f16(rng, (N, K), 0.02))
+    q, s = quantize_dev(B, w16, N, K)
+    w16.free()
+    algo = N * K + 4 * N + 2 * K + 2 * N
+    R = copies_for(N * K)
+    big = B.empty(R * N * K)
+    for r in range(R):
+        L.gpt2_d2d(big.at(r * N * K), q.ptr, N * K)
+    L.gpt2_sync()
+    ms_cold, _ = B.run_ops([B.op(3, y.ptr, x768.ptr, big.at(r * N * K), s.ptr, None, 1, N, K) for r in range(R)], 1, 5)
+    ms_cold /= R
+    ms_warm, _ = B.run_ops([B.op(3, y.ptr, x768.ptr, q.ptr, s.ptr, None, 1, N, K)], 10, 200)
+    res["head"] = {"N": N, "K": K, "bytes": algo, "copies": R,
+                   "cold_us": round(ms_cold * 1e3, 3), "cold_GBs": round(algo / (ms_cold * 1e-3) / 1e9, 1),
+                   "cold_frac_of_8TBs": round(algo / (ms_cold * 1e-3) / 8e12, 3),
+                   "warm_us": round(ms_warm * 1e3, 3), "warm_GBs": round(algo / (ms_warm * 1e-3) / 1e9, 1)}
+    big.free()
     # fp16 tied head: [1x768] . [768x50257], 77.3 MB
     N, K = VOCAB, 768
     algo = 2 * N * K + 2 * K + 2 * N
