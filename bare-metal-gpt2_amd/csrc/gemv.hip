@@ -188,13 +188,13 @@ struct GemvCfg {
 
 // First match on (row_chunks, qw) is the default; the rest are alternatives for tuning.
 static const GemvCfg kGv[] = {
-    G2_GV(16, 3, 1, true, 4),    // int8 K=768
+    G2_GV(16, 3, 2, true, 1),    // int8 K=768
+    G2_GV(16, 3, 1, true, 4),
     G2_GV(16, 12, 1, true, 4),   // int8 K=3072
     G2_GV(16, 6, 1, false, 4),   // fp16 K=768
     G2_GV(64, 6, 1, false, 4),   // fp16 K=3072
     G2_GV(16, 3, 2, true, 4),
     G2_GV(16, 3, 1, true, 1),
-    G2_GV(16, 3, 2, true, 1),
     G2_GV(64, 3, 1, true, 4),
     G2_GV(64, 3, 2, true, 4),
     G2_GV(32, 6, 1, true, 4),
