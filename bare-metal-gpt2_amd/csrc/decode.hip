@@ -85,12 +85,12 @@ constexpr int PD_SPIN = 1 << 15;                   // default poll rounds before
 constexpr int PH_CAND = 4 * GPT2_N_LAYER;
 
 // LDS layout (bytes).  Common: xs, xn, argmax scratch.  Attention work-groups: the q/k/v weight rows
-// they compute (QR rows, int8 or fp16), reused after the GEMV for the attention scratch; GEMV
-// work-groups: gelu(fc) and the attention words.
+// they compute (QR rows, always fp16: int8 rows are widened when they are staged), reused after the
+// GEMV for the attention scratch; GEMV work-groups: gelu(fc) and the attention words.
 constexpr int LDS_XS = 0, LDS_XN = LDS_XS + 2 * PD_E, LDS_MISC = LDS_XN + 2 * PD_E;   // misc: 512 B
 constexpr int LDS_ROLE = LDS_MISC + 512;
 template <bool Q8> struct Lds {
-    static constexpr int RB = Q8 ? PD_E : 2 * PD_E;       // bytes per q/k/v weight row
+    static constexpr int RB = 2 * PD_E;                   // bytes per q/k/v weight row (fp16)
     static constexpr int W = LDS_ROLE;                    // A: q/k/v weights, QR * RB
     static constexpr int QKVH = W + QR * RB;              // A: q, k slice, v slice (fp16)
     static constexpr int QSB = QKVH + 2 * QR;             // A: their scales and biases (fp32)
@@ -336,6 +336,39 @@ __device__ __forceinline__ void dma_qkv(char *lds_w, const void *W, int h, int s
     }
 }
 
+// The same QR rows from int8 codes, widened to exact fp16 on the way into LDS (same layout as
+// dma_qkv's fp16 rows).  The attention work-groups are idle while the GEMV phases run, so the
+// widening costs nothing on the critical path and the q/k/v GEMV then reads fp16 like the fp16 path.
+// Thread t handles 16-byte chunks t + 256m (m < 18) of the QR x 768 codes; the loads are all in
+// flight before the first is widened.
+__device__ __forceinline__ void stage_qkv_q8(char *lds_w, const void *W, int h, int sp, int tid) {
+    constexpr int CH = PD_E / 16, NCH = QR * CH, PER = NCH / PD_T;
+    static_assert(NCH % PD_T == 0, "whole chunks per thread");
+    const int8_t *Wb = reinterpret_cast<const int8_t *>(W);
+    uint4 v[PER];
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+        const int c = m * PD_T + tid, r = c / CH, k = c - r * CH;
+        v[m] = *reinterpret_cast<const uint4 *>(Wb + (size_t)qkv_row(h, sp, r) * PD_E + k * 16);
+    }
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+        const int c = m * PD_T + tid, r = c / CH, k = c - r * CH;
+        const uint32_t wd[4] = {v[m].x, v[m].y, v[m].z, v[m].w};
+        uint32_t o[8];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            f16x2 lo, hi;
+            i8x4_to_f16x4_v(wd[t], lo, hi);
+            o[2 * t] = __builtin_bit_cast(uint32_t, lo);
+            o[2 * t + 1] = __builtin_bit_cast(uint32_t, hi);
+        }
+        uint4 *dst = reinterpret_cast<uint4 *>(lds_w + r * 2 * PD_E + k * 32);
+        dst[0] = uint4{o[0], o[1], o[2], o[3]};
+        dst[1] = uint4{o[4], o[5], o[6], o[7]};
+    }
+}
+
 // Q8: every layer matrix is int8 codes with per-row scales (else every one is fp16).
 template <bool Q8>
 __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
@@ -386,7 +419,16 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
         float *qs = reinterpret_cast<float *>(lds + LY::QSB), *qb = qs + QR;
         float(*cl)[PD_D][8] = reinterpret_cast<float(*)[PD_D][8]>(lds + LY::CL);
         float(*pl)[64] = reinterpret_cast<float(*)[64]>(lds + LY::PL);
-        dma_qkv<LY::RB>(ldw, a.layers[0].w[0], h, sp, wave, lane);
+        // The embedding's loads go first: the memory counter completes in issue order, so loads
+        // issued after the weight DMA would have to wait for it.
+        uint16_t emb_t[3], emb_p[3];   // fp16 bits of wte[token], wpe[pos] at elements tid + 256i
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            emb_t[i] = a.wte[(size_t)token * PD_E + tid + PD_T * i];
+            emb_p[i] = a.wpe[(size_t)pos * PD_E + tid + PD_T * i];
+        }
+        if constexpr (Q8) stage_qkv_q8(ldw, a.layers[0].w[0], h, sp, tid);
+        else dma_qkv<LY::RB>(ldw, a.layers[0].w[0], h, sp, wave, lane);
         for (int l = 0; l < GPT2_N_LAYER; ++l) {
             const PDLayer &ly = a.layers[l];
             uint16_t *Kc = a.kv + (size_t)(2 * l) * PD_H * hstride + h * hstride;
@@ -417,18 +459,15 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             // ---- x: embed (layer 0) or the previous layer's output
             if (l == 0) {
 #pragma unroll
-                for (int i = 0; i < 3; ++i) {
-                    const int e = tid + PD_T * i;
-                    xs[e] = (f16)(h2f(a.wte[(size_t)token * PD_E + e]) + h2f(a.wpe[(size_t)pos * PD_E + e]));
-                }
-                __syncthreads();
+                for (int i = 0; i < 3; ++i) xs[tid + PD_T * i] = (f16)(h2f(emb_t[i]) + h2f(emb_p[i]));
+                lds_barrier();
             } else if (!read_x(seq(4 * l - 1), (l == 1 && a.trace) ? a.trace + wg * 128 + 122 : nullptr)) {
                 return;
             }
             mark(64 + 4 * l);
-            // This wave's weight DMA has landed (all waves: the barrier below).  It was issued before
-            // everything since, so all but the last XR operations is enough: those are the poll
-            // round of x still in flight, which need not be waited for.
+            // This wave's weight DMA (fp16 weights) has landed (all waves: the barrier below).  It was
+            // issued before everything since, so all but the last XR operations is enough: those are
+            // the poll round of x still in flight, which need not be waited for.
             wait_vm<XR>();
             if (l == 1) mark(113);
             if (tid < QR) {
@@ -437,46 +476,36 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             }
             layernorm768(xn, xs, lnp, lane);   // ends with a barrier
             if (l == 1) mark(114);
-            // ---- the QR rows: 16 lanes per row, 4 rows per wave per pass, two passes at a time
+            // ---- the QR rows: 16 lanes per row, 4 rows per wave per pass, two passes at a time.  Lane
+            // j reads six 8-element fp16 chunks of each row; for int8 weights the chunks follow the
+            // int8 layout (16 consecutive codes per 16-byte chunk j + 16i), so the products are summed
+            // in the same order as on the widened-in-registers path.
             {
-                constexpr int CPL = LY::RB / 256;          // 16-byte chunks per lane: 3 (int8), 6 (fp16)
                 const int j = lane & 15, rsl = lane >> 4;
-                // x elements of chunk j + 16i: int8 rows 16 per chunk (two f16x8), fp16 rows 8 (one)
+                auto eoff = [&](int i) { return Q8 ? (j + 16 * (i >> 1)) * 16 + 8 * (i & 1) : (j + 16 * i) * 8; };
                 f16x8 xr[6];
 #pragma unroll
-                for (int i = 0; i < 6; ++i)
-                    xr[i] = Q8 ? *reinterpret_cast<const f16x8 *>(xn + (j + 16 * (i >> 1)) * 16 + 8 * (i & 1))
-                               : *reinterpret_cast<const f16x8 *>(xn + (j + 16 * i) * 8);
-                auto dot = [&](const uint4(&w)[CPL]) {
+                for (int i = 0; i < 6; ++i) xr[i] = *reinterpret_cast<const f16x8 *>(xn + eoff(i));
+                auto dot = [&](const uint4(&w)[6]) {
                     float acc = 0.f;
 #pragma unroll
-                    for (int i = 0; i < CPL; ++i) {
+                    for (int i = 0; i < 6; ++i) {
                         const uint32_t wd[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
 #pragma unroll
-                        for (int t = 0; t < 4; ++t) {
-                            if constexpr (Q8) {
-                                f16x2 lo, hi;
-                                i8x4_to_f16x4_v(wd[t], lo, hi);
-                                const f16x8 &xv = xr[2 * i + (t >> 1)];
-                                const int o = (t & 1) * 4;
-                                acc = __builtin_amdgcn_fdot2(lo, f16x2{xv[o], xv[o + 1]}, acc, false);
-                                acc = __builtin_amdgcn_fdot2(hi, f16x2{xv[o + 2], xv[o + 3]}, acc, false);
-                            } else {
-                                acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, wd[t]),
-                                                             f16x2{xr[i][2 * t], xr[i][2 * t + 1]}, acc, false);
-                            }
-                        }
+                        for (int t = 0; t < 4; ++t)
+                            acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, wd[t]), f16x2{xr[i][2 * t], xr[i][2 * t + 1]},
+                                                         acc, false);
                     }
                     return acc;
                 };
 #pragma unroll
                 for (int p = 0; p < QR / 16; p += 2) {
                     const int ra = 16 * p + 4 * wave + rsl, rb2 = ra + 16;
-                    uint4 wa[CPL], wb[CPL];
+                    uint4 wa[6], wb[6];
 #pragma unroll
-                    for (int i = 0; i < CPL; ++i) {
-                        wa[i] = *reinterpret_cast<const uint4 *>(ldw + ra * LY::RB + (j + 16 * i) * 16);
-                        wb[i] = *reinterpret_cast<const uint4 *>(ldw + rb2 * LY::RB + (j + 16 * i) * 16);
+                    for (int i = 0; i < 6; ++i) {
+                        wa[i] = *reinterpret_cast<const uint4 *>(ldw + ra * LY::RB + 2 * eoff(i));
+                        wb[i] = *reinterpret_cast<const uint4 *>(ldw + rb2 * LY::RB + 2 * eoff(i));
                     }
                     float aa = dot(wa), ab = dot(wb);
                     aa = row16_sum(aa);
@@ -575,7 +604,10 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             if (l == 1) mark(118);
             lds_barrier();   // the attention scratch (aliasing the weights) is free again
             mark(4 * l);
-            if (l + 1 < GPT2_N_LAYER) dma_qkv<LY::RB>(ldw, a.layers[l + 1].w[0], h, sp, wave, lane);
+            if (l + 1 < GPT2_N_LAYER) {
+                if constexpr (Q8) stage_qkv_q8(ldw, a.layers[l + 1].w[0], h, sp, tid);
+                else dma_qkv<LY::RB>(ldw, a.layers[l + 1].w[0], h, sp, wave, lane);
+            }
         }
     } else if (wg - PD_NA < PD_NW) {
         // ================================ GEMV work-group g: proj, fc and mlp-proj rows
@@ -589,10 +621,11 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
         // Residual rows [g*RP, +RP) of x after the previous layer: this work-group wrote them itself
         // (its mlp-proj rows), layer 0 starts from the embedding.
         float xown[RP];
+        uint16_t emb_t[RP], emb_p[RP];   // fp16 bits, added once the first phase's input has arrived
 #pragma unroll
         for (int k = 0; k < RP; ++k) {
-            const int r = g * RP + k;
-            xown[k] = (float)(f16)(h2f(a.wte[(size_t)token * PD_E + r]) + h2f(a.wpe[(size_t)pos * PD_E + r]));
+            emb_t[k] = a.wte[(size_t)token * PD_E + g * RP + k];
+            emb_p[k] = a.wpe[(size_t)pos * PD_E + g * RP + k];
         }
         PhaseW<768, Q8, RP> WP;
         PhaseW<768, Q8, RF> WF;
@@ -606,6 +639,10 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                                                  [&](int i, uint32_t d) { part[i] = __uint_as_float(d); }))
                 return;
             mark(64 + 4 * l + 1);
+            if (l == 0) {
+#pragma unroll
+                for (int k = 0; k < RP; ++k) xown[k] = (float)(f16)(h2f(emb_t[k]) + h2f(emb_p[k]));
+            }
             load_phase(WF, ly.w[2], ly.s[2], ly.b[2], g * RF, wave, lane);
             LNParams lnp;
             load_ln(lnp, ly.ln2_g, ly.ln2_b);

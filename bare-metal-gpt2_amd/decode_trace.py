@@ -71,6 +71,10 @@ def main() -> None:
     t = tr.numpy(np.uint64, (256, 128)).astype(np.int64)
     rel = (t - t[:, 63].min()) * 0.01                  # us since the first work-group started
     print("shader clock %.3f GHz" % ((t[0, 127] - t[0, 126]) / ((t[0, 62] - t[0, 63]) * 10.0)))
+    st = rel[:, 63]
+    print("work-group start: median %.2f, max %.2f us (attention work-groups max %.2f); layer 0 attention "
+          "input %.2f us after its work-group started (median)" % (
+              np.median(st), st.max(), st[:NA].max(), np.median(rel[:NA, 64] - st[:NA])))
     names = ["attention", "proj", "fc", "mlp-proj"]
     sets = [slice(0, NA), slice(NA, NA + NG), slice(NA, NA + NG), slice(NA, NA + NG)]
     prev = 0.0
