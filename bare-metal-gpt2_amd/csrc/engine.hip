@@ -369,7 +369,7 @@ extern "C" void gpt2_prefill_fill_cache(const GPT2Backend *be, const GPT2Weights
 // ============================================================================ graph replay
 struct GPT2DecodeGraph {
     hipStream_t stream;
-    hipGraph_t graph;
+    hipGraph_t graph;       // multi-kernel mode only
     hipGraphExec_t exec;
     int *state;       // device {token, pos, epoch, error}
     GPT2KVCache *kv;
@@ -422,11 +422,13 @@ extern "C" GPT2DecodeGraph *gpt2_decode_graph_create_mode(const GPT2Backend *be,
     }
 
     hipStream_t prev = stream();
+    // The persistent step is one kernel: it is launched directly (a one-node graph only adds launch
+    // latency, measured ~8 us per replay); the multi-kernel step is captured once and replayed.
+    if (g->mode == GPT2_DECODE_PERSISTENT) return g;
     gpt2_set_stream(g->stream);
     hipError_t e = hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal);
     if (e == hipSuccess) {
-        if (g->mode == GPT2_DECODE_PERSISTENT) persist_launch(g->plan, g->stream);
-        else decode_step(be, w, kv, StepArg{0, 0, g->state}, s, logits, nullptr, g->state, tokens);
+        decode_step(be, w, kv, StepArg{0, 0, g->state}, s, logits, nullptr, g->state, tokens);
         e = hipStreamEndCapture(g->stream, &g->graph);
     }
     gpt2_set_stream(prev);
@@ -460,8 +462,14 @@ extern "C" int gpt2_decode_graph_run(GPT2DecodeGraph *g, int steps) {
     if (!g || steps < 0) { set_error(E_ARG, "gpt2_decode_graph_run"); return 1; }
     if (g->host_pos + steps > g->kv->maxT) { set_error(E_CAPACITY, "gpt2_decode_graph_run: past the cache"); return 1; }
     for (int i = 0; i < steps; ++i) {
-        hipError_t e = hipGraphLaunch(g->exec, g->stream);
-        if (e != hipSuccess) { set_error((int)e, "hipGraphLaunch"); return (int)e; }
+        hipError_t e;
+        if (g->mode == GPT2_DECODE_PERSISTENT) {
+            persist_launch(g->plan, g->stream);
+            e = hipGetLastError();
+        } else {
+            e = hipGraphLaunch(g->exec, g->stream);
+        }
+        if (e != hipSuccess) { set_error((int)e, "decode step launch"); return (int)e; }
     }
     g->host_pos += steps;
     return 0;
@@ -506,8 +514,8 @@ extern "C" int gpt2_decode_graph_time(GPT2DecodeGraph *g, int steps, float *ms) 
 extern "C" void gpt2_decode_graph_destroy(GPT2DecodeGraph *g) {
     if (!g) return;
     hipStreamSynchronize(g->stream);
-    hipGraphExecDestroy(g->exec);
-    hipGraphDestroy(g->graph);
+    if (g->exec) hipGraphExecDestroy(g->exec);
+    if (g->graph) hipGraphDestroy(g->graph);
     graph_free(g);
 }
 
