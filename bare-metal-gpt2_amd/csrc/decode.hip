@@ -74,11 +74,23 @@ static_assert(PD_G == PD_T, "the final argmax gives each thread one work-group's
 static_assert(PD_S * 4 * 64 >= GPT2_N_CTX, "an attention wave holds at most 64 keys of a full cache");
 
 // Exchange arena (64-bit flag words).
+// Each writing work-group's words start on their own 128-byte line (16 words): lines written by
+// work-groups on different XCDs were measurably slower to become visible.
+constexpr int LINE = 16;                           // words per 128-byte line
+constexpr int pad_line(int n) { return (n + LINE - 1) / LINE * LINE; }
+constexpr int XS_W = pad_line(RP);                 // x: RP words per GEMV work-group
+constexpr int AT_W = pad_line(PD_PW);              // attention: PW words per attention work-group
+constexpr int HD_W = pad_line(RF / 2);             // gelu(fc): RF/2 words (fp16 pairs) per GEMV work-group
 constexpr int LL_X = 0;                            // residual stream: 768 words, one fp16 each
-constexpr int LL_ATT = LL_X + PD_E;                // attention: NA*PW words, fp32
-constexpr int LL_HID = LL_ATT + PD_NA * PD_PW;     // gelu(fc): 1536 words, two fp16 each
-constexpr int LL_CAND = LL_HID + PD_F / 2;         // argmax candidates: G words
-constexpr int LL_WORDS = LL_CAND + PD_G;
+constexpr int LL_ATT = LL_X + PD_NW * XS_W;        // attention: NA*PW words, fp32
+constexpr int LL_HID = LL_ATT + PD_NA * AT_W;      // gelu(fc): 1536 words, two fp16 each
+constexpr int LL_CAND = LL_HID + PD_NW * HD_W;     // argmax candidates: one word per work-group
+constexpr int LL_WORDS = LL_CAND + PD_G * LINE;
+// word of element i of each buffer
+__device__ __forceinline__ int x_word(int i) { return (i / RP) * XS_W + i % RP; }
+__device__ __forceinline__ int at_word(int i) { return (i / PD_PW) * AT_W + i % PD_PW; }
+__device__ __forceinline__ int hd_word(int i) { return (i / (RF / 2)) * HD_W + i % (RF / 2); }
+__device__ __forceinline__ int cand_word(int i) { return i * LINE; }
 constexpr int PD_SPIN = 1 << 15;                   // default poll rounds before a work-group gives up
 // Phase numbers (sequence = epoch*64 + phase): per layer l, 4l attention, 4l+1 x after proj,
 // 4l+2 gelu(fc), 4l+3 x after mlp-proj; 48 head candidates.
@@ -111,19 +123,20 @@ __device__ __forceinline__ void ll_st(uint64_t *p, uint32_t data, uint32_t flag)
     __hip_atomic_store(p, ((uint64_t)flag << 32) | data, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Polls words [0, n) of `base` (R per thread, word tid + 256r; all loads in flight before any check)
+// Polls elements [0, n) of `base` (R per thread, element tid + 256r at word idx(i); all loads in
+// flight before any check)
 // until every flag equals `flag`, then calls sink(i, data).  Returns false (for the whole
 // work-group) if a word did not arrive within `spin` rounds or another work-group reported an
 // error; the caller then leaves.  wflag: 4 ints of LDS for the work-group's verdict; dbg (optional,
 // profiling): thread 0 stores the start time and the number of extra poll rounds there.
 static_assert(PD_T == 256, "ll_read combines four waves");
-template <int R, class Sink>
-__device__ bool ll_read(const uint64_t *base, int n, uint32_t flag, int *err, int spin, int *wflag, Sink sink,
-                        unsigned long long *dbg = nullptr) {
+template <int R, class Idx, class Sink>
+__device__ bool ll_read(const uint64_t *base, int n, uint32_t flag, int *err, int spin, int *wflag, Idx idx,
+                        Sink sink, unsigned long long *dbg = nullptr) {
     if (dbg && threadIdx.x == 0) dbg[0] = __builtin_amdgcn_s_memrealtime();
     uint64_t v[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) v[r] = ll_ld(base + min((int)threadIdx.x + PD_T * r, n - 1));
+    for (int r = 0; r < R; ++r) v[r] = ll_ld(base + idx(min((int)threadIdx.x + PD_T * r, n - 1)));
     bool bad = false;
     for (int round = 0;; ++round) {
         bool ok = true;
@@ -141,7 +154,7 @@ __device__ bool ll_read(const uint64_t *base, int n, uint32_t flag, int *err, in
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int i = threadIdx.x + PD_T * r;
-            if (i < n && (uint32_t)(v[r] >> 32) != flag) v[r] = ll_ld(base + i);
+            if (i < n && (uint32_t)(v[r] >> 32) != flag) v[r] = ll_ld(base + idx(i));
         }
     }
     // The loop is wave-uniform, so `bad` is too.  Barriers here wait for LDS traffic only, so they
@@ -397,7 +410,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     const size_t hstride = (size_t)a.maxT * PD_D;
 
     auto read_x = [&](uint32_t flag, unsigned long long *dbg = nullptr) {
-        return ll_read<XR>(LX, PD_E, flag, a.err, a.spin, wflag,
+        return ll_read<XR>(LX, PD_E, flag, a.err, a.spin, wflag, x_word,
                           [&](int i, uint32_t d) { xs[i] = __builtin_bit_cast(f16, (uint16_t)d); }, dbg);
     };
 
@@ -599,7 +612,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 } else {
                     val = (float)qkvh[PD_D + KS + (tid - 3 - PD_D)];
                 }
-                ll_st(LA + wg * PD_PW + tid, __float_as_uint(val), seq(4 * l));
+                ll_st(LA + at_word(wg * PD_PW + tid), __float_as_uint(val), seq(4 * l));
             }
             if (l == 1) mark(118);
             lds_barrier();   // the attention scratch (aliasing the weights) is free again
@@ -612,9 +625,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     } else if (wg - PD_NA < PD_NW) {
         // ================================ GEMV work-group g: proj, fc and mlp-proj rows
         // A work-group polls a buffer only in a phase it writes from, so every writer of the next
-        // version of a buffer has first read everything its readers needed.  Each phase's weight
-        // rows are loaded while the phase before it runs (after that phase's input has arrived, so
-        // the polls never queue behind weight loads).
+        // version of a buffer has first read everything its readers needed.
         const int g = wg - PD_NA;
         f16 *hs = reinterpret_cast<f16 *>(lds + LY::HS);
         float *part = reinterpret_cast<float *>(lds + LY::PART);
@@ -627,15 +638,22 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             emb_t[k] = a.wte[(size_t)token * PD_E + g * RP + k];
             emb_p[k] = a.wpe[(size_t)pos * PD_E + g * RP + k];
         }
+        // A layer's proj, fc and mlp-proj rows (and LN2 params) are all in flight before the
+        // layer's first input arrives: issued right after the previous layer's last poll (the
+        // mlp-proj rows after its mlp-proj, whose registers they reuse).  Loads complete in issue
+        // order, so a weight load issued shortly before a poll would hold that poll back.
         PhaseW<768, Q8, RP> WP;
         PhaseW<768, Q8, RF> WF;
         PhaseW<3072, Q8, RM> WM;
+        LNParams lnp;
         load_phase(WP, a.layers[0].w[1], a.layers[0].s[1], a.layers[0].b[1], g * RP, wave, lane);
+        load_phase(WF, a.layers[0].w[2], a.layers[0].s[2], a.layers[0].b[2], g * RF, wave, lane);
+        load_ln(lnp, a.layers[0].ln2_g, a.layers[0].ln2_b);
+        load_phase(WM, a.layers[0].w[3], a.layers[0].s[3], a.layers[0].b[3], g * RM, wave, lane);
         for (int l = 0; l < GPT2_N_LAYER; ++l) {
-            const PDLayer &ly = a.layers[l];
             // ---- P: combine the attention words, proj rows, + bias + residual
             constexpr int NA = PD_NA * PD_PW;
-            if (!ll_read<(NA + PD_T - 1) / PD_T>(LA, NA, seq(4 * l), a.err, a.spin, wflag,
+            if (!ll_read<(NA + PD_T - 1) / PD_T>(LA, NA, seq(4 * l), a.err, a.spin, wflag, at_word,
                                                  [&](int i, uint32_t d) { part[i] = __uint_as_float(d); }))
                 return;
             mark(64 + 4 * l + 1);
@@ -643,9 +661,6 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
 #pragma unroll
                 for (int k = 0; k < RP; ++k) xown[k] = (float)(f16)(h2f(emb_t[k]) + h2f(emb_p[k]));
             }
-            load_phase(WF, ly.w[2], ly.s[2], ly.b[2], g * RF, wave, lane);
-            LNParams lnp;
-            load_ln(lnp, ly.ln2_g, ly.ln2_b);
             // Element e = tid + 256i: wave w handles head w + 4i, so the per-head weights are
             // wave-uniform; every lane computes them (broadcast LDS reads, no branches).
             static_assert(PD_S == 4 && PD_T / PD_D == 4, "four slices per head, one head per wave and element");
@@ -682,13 +697,12 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             lds_barrier();
             if (l == 1) mark(119);
             run_phase(WP, xn, wave, lane, [&](int k, float v) {
-                if (lane == 0) ll_st(LX + g * RP + k, __builtin_bit_cast(uint16_t, (f16)(v + xown[k])), seq(4 * l + 1));
+                if (lane == 0) ll_st(LX + x_word(g * RP + k), __builtin_bit_cast(uint16_t, (f16)(v + xown[k])), seq(4 * l + 1));
             });
             mark(4 * l + 1);
             // ---- F: LN2 + fc rows [g*RF, +RF) + gelu, exchanged in pairs
             if (!read_x(seq(4 * l + 1))) return;
             mark(64 + 4 * l + 2);
-            load_phase(WM, ly.w[3], ly.s[3], ly.b[3], g * RM, wave, lane);
             layernorm768(xn, xs, lnp, lane);
             if (l == 1) mark(120);
             run_phase(WF, xn, wave, lane, [&](int k, float v) {
@@ -697,24 +711,30 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             if (l == 1) mark(121);
             lds_barrier();
             if (tid < RF / 2)
-                ll_st(LHd + g * RF / 2 + tid, (uint32_t)hout[2 * tid] | ((uint32_t)hout[2 * tid + 1] << 16), seq(4 * l + 2));
+                ll_st(LHd + hd_word(g * RF / 2 + tid), (uint32_t)hout[2 * tid] | ((uint32_t)hout[2 * tid + 1] << 16), seq(4 * l + 2));
             mark(4 * l + 2);
             // ---- M: mlp-proj rows [g*RM, +RM) over gelu(fc), + bias + residual
-            if (!ll_read<PD_F / 2 / PD_T>(LHd, PD_F / 2, seq(4 * l + 2), a.err, a.spin, wflag,
+            if (!ll_read<PD_F / 2 / PD_T>(LHd, PD_F / 2, seq(4 * l + 2), a.err, a.spin, wflag, hd_word,
                                           [&](int i, uint32_t d) {
                                               hs[2 * i] = __builtin_bit_cast(f16, (uint16_t)(d & 0xffff));
                                               hs[2 * i + 1] = __builtin_bit_cast(f16, (uint16_t)(d >> 16));
                                           }))
                 return;
             mark(64 + 4 * l + 3);
-            if (l + 1 < GPT2_N_LAYER)
-                load_phase(WP, a.layers[l + 1].w[1], a.layers[l + 1].s[1], a.layers[l + 1].b[1], g * RP, wave, lane);
+            const bool next = l + 1 < GPT2_N_LAYER;
+            if (next) {
+                const PDLayer &ln = a.layers[l + 1];
+                load_phase(WP, ln.w[1], ln.s[1], ln.b[1], g * RP, wave, lane);
+                load_phase(WF, ln.w[2], ln.s[2], ln.b[2], g * RF, wave, lane);
+                load_ln(lnp, ln.ln2_g, ln.ln2_b);
+            }
             run_phase(WM, hs, wave, lane, [&](int k, float v) {
                 const int r = g * RM + k;
                 const f16 o = (f16)(v + (float)xs[r]);
                 xown[k] = (float)o;
-                if (lane == 0) ll_st(LX + r, __builtin_bit_cast(uint16_t, o), seq(4 * l + 3));
+                if (lane == 0) ll_st(LX + x_word(r), __builtin_bit_cast(uint16_t, o), seq(4 * l + 3));
             });
+            if (next) load_phase(WM, a.layers[l + 1].w[3], a.layers[l + 1].s[3], a.layers[l + 1].b[3], g * RM, wave, lane);
             mark(4 * l + 3);
         }
     }
@@ -820,12 +840,12 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             if (bv[w] > best || (bv[w] == best && bi[w] < bidx)) { best = bv[w]; bidx = bi[w]; }
         const uint32_t cand = (bidx == 0x7fffffff) ? 0xffffu
                                                    : ((uint32_t)__builtin_bit_cast(uint16_t, (f16)best) << 16) | (uint32_t)bidx;
-        ll_st(LC + wg, cand, seq(ph));
+        ll_st(LC + cand_word(wg), cand, seq(ph));
     }
     if (wg != 0) return;
     // work-group 0: argmax over the candidates, advance the state
     uint32_t *cands = reinterpret_cast<uint32_t *>(lds + LY::CANDS);
-    if (!ll_read<(PD_G + PD_T - 1) / PD_T>(LC, PD_G, seq(ph), a.err, a.spin, wflag,
+    if (!ll_read<(PD_G + PD_T - 1) / PD_T>(LC, PD_G, seq(ph), a.err, a.spin, wflag, cand_word,
                                           [&](int i, uint32_t d) { cands[i] = d; }))
         return;
     {
