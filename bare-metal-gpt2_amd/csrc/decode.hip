@@ -394,7 +394,8 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     float *sm = reinterpret_cast<float *>(lds + LDS_MISC + 32), *sl = reinterpret_cast<float *>(lds + LDS_MISC + 48);
     uint16_t *hout = reinterpret_cast<uint16_t *>(lds + LDS_MISC + 64);   // RF values
     int *wflag = reinterpret_cast<int *>(lds + LDS_MISC + 96);             // ll_read verdicts, 4 ints
-    static_assert(64 + 2 * RF <= 96, "LDS misc layout");
+    uint32_t *xout = reinterpret_cast<uint32_t *>(lds + LDS_MISC + 112);   // RP x words, one store
+    static_assert(64 + 2 * RF <= 96 && 112 + 4 * RP <= 512, "LDS misc layout");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wg = blockIdx.x;
     const int token = a.state[0], pos = a.state[1];
@@ -696,9 +697,12 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             if (l == 1) mark(118);
             lds_barrier();
             if (l == 1) mark(119);
+            // the RP rows' words go out as one store (one instruction, one line)
             run_phase(WP, xn, wave, lane, [&](int k, float v) {
-                if (lane == 0) ll_st(LX + x_word(g * RP + k), __builtin_bit_cast(uint16_t, (f16)(v + xown[k])), seq(4 * l + 1));
+                if (lane == 0) xout[k] = __builtin_bit_cast(uint16_t, (f16)(v + xown[k]));
             });
+            lds_barrier();
+            if (tid < RP) ll_st(LX + x_word(g * RP + tid), xout[tid], seq(4 * l + 1));
             mark(4 * l + 1);
             // ---- F: LN2 + fc rows [g*RF, +RF) + gelu, exchanged in pairs
             if (!read_x(seq(4 * l + 1))) return;
@@ -729,11 +733,12 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 load_ln(lnp, ln.ln2_g, ln.ln2_b);
             }
             run_phase(WM, hs, wave, lane, [&](int k, float v) {
-                const int r = g * RM + k;
-                const f16 o = (f16)(v + (float)xs[r]);
+                const f16 o = (f16)(v + (float)xs[g * RM + k]);
                 xown[k] = (float)o;
-                if (lane == 0) ll_st(LX + x_word(r), __builtin_bit_cast(uint16_t, o), seq(4 * l + 3));
+                if (lane == 0) xout[k] = __builtin_bit_cast(uint16_t, o);
             });
+            lds_barrier();
+            if (tid < RM) ll_st(LX + x_word(g * RM + tid), xout[tid], seq(4 * l + 3));
             if (next) load_phase(WM, a.layers[l + 1].w[3], a.layers[l + 1].s[3], a.layers[l + 1].b[3], g * RM, wave, lane);
             mark(4 * l + 3);
         }
