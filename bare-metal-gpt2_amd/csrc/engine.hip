@@ -367,9 +367,11 @@ extern "C" void gpt2_prefill_fill_cache(const GPT2Backend *be, const GPT2Weights
 }
 
 // ============================================================================ graph replay
+constexpr int PERSIST_CHUNK = 16;   // persistent steps per graph replay
+
 struct GPT2DecodeGraph {
     hipStream_t stream;
-    hipGraph_t graph;       // multi-kernel mode only
+    hipGraph_t graph;       // one step (multi-kernel) or PERSIST_CHUNK steps (persistent)
     hipGraphExec_t exec;
     int *state;       // device {token, pos, epoch, error}
     GPT2KVCache *kv;
@@ -422,13 +424,16 @@ extern "C" GPT2DecodeGraph *gpt2_decode_graph_create_mode(const GPT2Backend *be,
     }
 
     hipStream_t prev = stream();
-    // The persistent step is one kernel: it is launched directly (a one-node graph only adds launch
-    // latency, measured ~8 us per replay); the multi-kernel step is captured once and replayed.
-    if (g->mode == GPT2_DECODE_PERSISTENT) return g;
+    // The multi-kernel step is captured once and replayed per token.  The persistent step is one
+    // kernel: PERSIST_CHUNK consecutive steps are captured as one graph (one replay decodes that many
+    // tokens), and single steps or the remainder of a run are launched directly (a one-kernel graph
+    // per token only adds launch latency, ~8 us measured).
     gpt2_set_stream(g->stream);
     hipError_t e = hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal);
     if (e == hipSuccess) {
-        decode_step(be, w, kv, StepArg{0, 0, g->state}, s, logits, nullptr, g->state, tokens);
+        if (g->mode == GPT2_DECODE_PERSISTENT)
+            for (int i = 0; i < PERSIST_CHUNK; ++i) persist_launch(g->plan, g->stream);
+        else decode_step(be, w, kv, StepArg{0, 0, g->state}, s, logits, nullptr, g->state, tokens);
         e = hipStreamEndCapture(g->stream, &g->graph);
     }
     gpt2_set_stream(prev);
@@ -461,13 +466,18 @@ extern "C" int gpt2_decode_graph_set(GPT2DecodeGraph *g, int token, int pos) {
 extern "C" int gpt2_decode_graph_run(GPT2DecodeGraph *g, int steps) {
     if (!g || steps < 0) { set_error(E_ARG, "gpt2_decode_graph_run"); return 1; }
     if (g->host_pos + steps > g->kv->maxT) { set_error(E_CAPACITY, "gpt2_decode_graph_run: past the cache"); return 1; }
-    for (int i = 0; i < steps; ++i) {
+    for (int i = 0; i < steps;) {
         hipError_t e;
-        if (g->mode == GPT2_DECODE_PERSISTENT) {
+        if (g->mode != GPT2_DECODE_PERSISTENT) {
+            e = hipGraphLaunch(g->exec, g->stream);
+            ++i;
+        } else if (steps - i >= PERSIST_CHUNK) {
+            e = hipGraphLaunch(g->exec, g->stream);
+            i += PERSIST_CHUNK;
+        } else {
             persist_launch(g->plan, g->stream);
             e = hipGetLastError();
-        } else {
-            e = hipGraphLaunch(g->exec, g->stream);
+            ++i;
         }
         if (e != hipSuccess) { set_error((int)e, "decode step launch"); return (int)e; }
     }

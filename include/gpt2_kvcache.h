@@ -77,8 +77,9 @@ GPT2DecodeGraph *gpt2_decode_graph_create(const GPT2Backend *be, const GPT2Weigh
  *                           backend slots (int8 / gemv backends) and the GPU to itself while a step
  *                           runs (its work-groups must be resident together; if they are not, the
  *                           step gives up after a bounded wait and gpt2_decode_graph_sync reports
- *                           an error).  Being one kernel, it is launched directly on the private
- *                           stream rather than through a one-node graph;
+ *                           an error).  Being one kernel per token, 16 consecutive steps are
+ *                           captured as one graph (one replay decodes 16 tokens); single steps and
+ *                           the rest of a run are launched directly on the private stream;
  *   GPT2_DECODE_AUTO        persistent when the backend allows it (env GPT2_DECODE_PERSISTENT=0
  *                           forces the multi-kernel step).
  * gpt2_decode_graph_create uses GPT2_DECODE_AUTO.  No reference counterpart. */
