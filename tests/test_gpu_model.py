@@ -378,6 +378,50 @@ def test_persistent_decode_deterministic_free_run(pkg, L, synth, model):
         model.gpu.q = None
 
 
+def test_persistent_decode_positions(pkg, L, synth, model):
+    """Key-split edge cases of the persistent step: position 0 (no earlier keys, every split empty),
+    small contexts where some splits or waves get no keys, splits that do not divide evenly, and the
+    last slots of a full 1024-row cache (each attention wave then holds 64 keys, its register
+    capacity).  Each position is teacher-forced against the eager step on the same cache prefix (a
+    1023-token prefill); gates as in test_persistent_decode_matches_eager."""
+    model.quantize()
+    try:
+        ids = synth.token_ids(1023, seed=23)
+        kv, scr, logits = decode_setup(pkg, L, model, ids, "int8")
+        be = pkg.backend("int8")
+        tokens = pkg.Dev(1024 * 4)
+        g = L.gpt2_decode_graph_create_mode(be, C.byref(model.gpu), C.byref(kv.kv), C.byref(scr.s), logits.ptr,
+                                            tokens.ptr, pkg.DECODE_PERSISTENT)
+        assert g, pkg.check("graph create")
+        try:
+            assert L.gpt2_decode_graph_mode(g) == pkg.DECODE_PERSISTENT
+            tok, pos = C.c_int(), C.c_int()
+            for p in (0, 1, 2, 3, 4, 5, 7, 8, 9, 13, 63, 64, 65, 255, 256, 257, 511, 777, 1000, 1021, 1022, 1023):
+                tok_in = int(ids[p]) if p < len(ids) else 17
+                kv.kv.len = len(ids)
+                L.gpt2_decode_step_cuda(be, C.byref(model.gpu), C.byref(kv.kv), tok_in, p, C.byref(scr.s),
+                                        logits.ptr, None)
+                pkg.check("eager step")
+                ref16 = logits.numpy(np.uint16, (V,)).copy()
+                assert L.gpt2_decode_graph_set(g, tok_in, p) == 0
+                assert L.gpt2_decode_graph_run(g, 1) == 0
+                assert L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)) == 0, pkg.check("persistent step")
+                assert pos.value == p + 1
+                lg = logits.numpy(np.uint16, (V,))
+                got, ref = oracle.f16_to_f32(lg)[None], oracle.f16_to_f32(ref16)[None]
+                assert rel_err(got, ref) <= 1e-2, (p, rel_err(got, ref))
+                assert kl_rows(ref, got).max() < 2e-3, p
+                assert tok.value == first_argmax(lg), p
+        finally:
+            L.gpt2_decode_graph_destroy(g)
+        scr.free()
+        kv.free()
+    finally:
+        L.gpt2_quant_free(C.byref(model.q))
+        model.q = None
+        model.gpu.q = None
+
+
 def test_persistent_decode_falls_back_without_gemv(pkg, L, synth, model):
     """Backends without this library's GEMV slots (flash: M=1 matmul fallback) get the multi-kernel
     step even when the persistent one is requested."""
