@@ -61,7 +61,10 @@ constexpr int PD_NA = PD_H * PD_S;                 // attention work-groups: 0 .
 constexpr int PD_NG = PD_G - PD_NA;                // GEMV work-groups: NA .. G-1
 constexpr int KS = PD_D / PD_S;                    // k and v rows of key `pos` per attention work-group
 constexpr int QR = PD_D + 2 * KS;                  // rows it computes: q (64), its k slice, its v slice
-constexpr int PD_PW = 2 + PD_D + 1 + KS;           // words it sends: m, l, c[64], its q.k part, its v slice
+// Words an attention work-group sends: m and l (fp32), c/l (its 64 context values divided by l: a
+// weighted mean of values) as 32 fp16 pairs, its part of q.k_pos (fp32), its v_pos slice as fp16 pairs.
+constexpr int AW_M = 0, AW_L = 1, AW_C = 2, AW_S = AW_C + PD_D / 2, AW_V = AW_S + 1;
+constexpr int PD_PW = AW_V + KS / 2;
 constexpr int RP = 4, RF = 16, RM = 4;             // rows per GEMV work-group: proj, fc, mlp-proj
 constexpr int PD_NW = PD_E / RP;                   // GEMV work-groups with rows (the rest wait for the head)
 constexpr int RH = (PD_V + PD_G - 1) / PD_G;       // head rows per work-group (the last has fewer)
@@ -579,8 +582,8 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             lds_barrier();
             if (l == 1) mark(117);
             if (tid < PD_PW) {
-                float val = 0.f;
-                if (tid < 2 + PD_D) {
+                uint32_t val = 0;
+                if (tid < AW_S) {
                     // the four waves' partials merged, branch-free (independent LDS reads)
                     float mw[4], lw[4], fw[4];
 #pragma unroll
@@ -591,29 +594,42 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                     float mx = -INFINITY;
 #pragma unroll
                     for (int w = 0; w < 4; ++w) mx = (lw[w] != 0.f) ? fmaxf(mx, mw[w]) : mx;
+                    float lsum = 0.f;
 #pragma unroll
-                    for (int w = 0; w < 4; ++w) fw[w] = (lw[w] != 0.f) ? __expf(mw[w] - mx) : 0.f;
-                    if (tid == 0) {
-                        val = mx;
-                    } else if (tid == 1) {
-#pragma unroll
-                        for (int w = 0; w < 4; ++w) val += lw[w] * fw[w];
-                    } else {
-#pragma unroll
-                        for (int w = 0; w < 4; ++w) {
-                            const float4 ca = *reinterpret_cast<const float4 *>(&cl[w][tid - 2][0]);
-                            const float4 cb = *reinterpret_cast<const float4 *>(&cl[w][tid - 2][4]);
-                            val += (((ca.x + ca.y) + (ca.z + ca.w)) + ((cb.x + cb.y) + (cb.z + cb.w))) * fw[w];
-                        }
+                    for (int w = 0; w < 4; ++w) {
+                        fw[w] = (lw[w] != 0.f) ? __expf(mw[w] - mx) : 0.f;
+                        lsum += lw[w] * fw[w];
                     }
-                } else if (tid == 2 + PD_D) {
-                    // q[KS*sp ..] . k_pos[KS*sp ..] in fp32 from the fp16 values
+                    if (tid == AW_M) {
+                        val = __float_as_uint(mx);
+                    } else if (tid == AW_L) {
+                        val = __float_as_uint(lsum);
+                    } else {
+                        const int d0 = 2 * (tid - AW_C);
+                        float c2[2] = {0.f, 0.f};
 #pragma unroll
-                    for (int i = 0; i < KS; ++i) val += (float)qkvh[KS * sp + i] * (float)qkvh[PD_D + i];
+                        for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+                            for (int w = 0; w < 4; ++w) {
+                                const float4 ca = *reinterpret_cast<const float4 *>(&cl[w][d0 + h2][0]);
+                                const float4 cb = *reinterpret_cast<const float4 *>(&cl[w][d0 + h2][4]);
+                                c2[h2] += (((ca.x + ca.y) + (ca.z + ca.w)) + ((cb.x + cb.y) + (cb.z + cb.w))) * fw[w];
+                            }
+                        const float inv = lsum != 0.f ? 1.0f / lsum : 0.f;
+                        val = (uint32_t)f2h(c2[0] * inv) | ((uint32_t)f2h(c2[1] * inv) << 16);
+                    }
+                } else if (tid == AW_S) {
+                    // q[KS*sp ..] . k_pos[KS*sp ..] in fp32 from the fp16 values
+                    float d = 0.f;
+#pragma unroll
+                    for (int i = 0; i < KS; ++i) d += (float)qkvh[KS * sp + i] * (float)qkvh[PD_D + i];
+                    val = __float_as_uint(d);
                 } else {
-                    val = (float)qkvh[PD_D + KS + (tid - 3 - PD_D)];
+                    const int i = 2 * (tid - AW_V);
+                    val = (uint32_t)__builtin_bit_cast(uint16_t, qkvh[PD_D + KS + i]) |
+                          ((uint32_t)__builtin_bit_cast(uint16_t, qkvh[PD_D + KS + i + 1]) << 16);
                 }
-                ll_st(LA + at_word(wg * PD_PW + tid), __float_as_uint(val), seq(4 * l));
+                ll_st(LA + at_word(wg * PD_PW + tid), val, seq(4 * l));
             }
             if (l == 1) mark(118);
             lds_barrier();   // the attention scratch (aliasing the weights) is free again
@@ -663,8 +679,13 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 for (int k = 0; k < RP; ++k) xown[k] = (float)(f16)(h2f(emb_t[k]) + h2f(emb_p[k]));
             }
             // Element e = tid + 256i: wave w handles head w + 4i, so the per-head weights are
-            // wave-uniform; every lane computes them (broadcast LDS reads, no branches).
+            // wave-uniform; every lane computes them (broadcast LDS reads, no branches).  Key `pos` is
+            // one more partial: m = q.k_pos / 8 from the four slices' parts, l = 1, c = v_pos.
             static_assert(PD_S == 4 && PD_T / PD_D == 4, "four slices per head, one head per wave and element");
+            auto half_of = [](float w, int hi) {
+                const uint32_t u = __float_as_uint(w);
+                return h2f((uint16_t)(hi ? u >> 16 : u & 0xffff));
+            };
 #pragma unroll
             for (int i = 0; i < 3; ++i) {
                 const int e = tid + PD_T * i, hh = e / PD_D, d = e % PD_D;
@@ -672,24 +693,23 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 float m4[PD_S], l4[PD_S], s4[PD_S], f4[PD_S], c4[PD_S];
 #pragma unroll
                 for (int s2 = 0; s2 < PD_S; ++s2) {
-                    m4[s2] = p[s2 * PD_PW];
-                    l4[s2] = p[s2 * PD_PW + 1];
-                    s4[s2] = p[s2 * PD_PW + 2 + PD_D];
-                    c4[s2] = p[s2 * PD_PW + 2 + d];
+                    m4[s2] = p[s2 * PD_PW + AW_M];
+                    l4[s2] = p[s2 * PD_PW + AW_L];
+                    s4[s2] = p[s2 * PD_PW + AW_S];
+                    c4[s2] = half_of(p[s2 * PD_PW + AW_C + d / 2], d & 1);   // c / l of split s2
                 }
-                const float vpos = p[(d / KS) * PD_PW + 3 + PD_D + d % KS];
-                // key `pos`: m = q.k_pos / 8 from the four slices' parts, l = 1, c = v_pos
+                const float vpos = half_of(p[(d / KS) * PD_PW + AW_V + (d % KS) / 2], d & 1);
                 const float spos = ((s4[0] + s4[1]) + (s4[2] + s4[3])) * 0.125f;
                 float mx = spos;
 #pragma unroll
                 for (int s2 = 0; s2 < PD_S; ++s2) mx = (l4[s2] != 0.f) ? fmaxf(mx, m4[s2]) : mx;
 #pragma unroll
-                for (int s2 = 0; s2 < PD_S; ++s2) f4[s2] = (l4[s2] != 0.f) ? __expf(m4[s2] - mx) : 0.f;
+                for (int s2 = 0; s2 < PD_S; ++s2) f4[s2] = (l4[s2] != 0.f) ? __expf(m4[s2] - mx) * l4[s2] : 0.f;
                 float L = __expf(spos - mx);
                 float c = L * vpos;
 #pragma unroll
                 for (int s2 = 0; s2 < PD_S; ++s2) {
-                    L += l4[s2] * f4[s2];
+                    L += f4[s2];
                     c += c4[s2] * f4[s2];
                 }
                 xn[e] = (f16)(c / L);
