@@ -9,7 +9,8 @@
 extern "C" {
 
 // One timed operation: kind 0 = fp16 GEMM (gpt2_matmul_tiled), 1 = INT8 GEMM (gpt2_matmul_int8),
-// 2 = fp16 GEMV (gpt2_gemv_fp16), 3 = INT8 GEMV (gpt2_gemv_int8).
+// 2 = fp16 GEMV (gpt2_gemv_fp16), 3 = INT8 GEMV (gpt2_gemv_int8), 4 = causal prefill attention
+// (gpt2_attention_flash: C = att, A = qkv, M = T).
 typedef struct {
     int kind;
     gpt2_half *C;
@@ -25,6 +26,7 @@ static void run_op(const GPT2BenchOp &o) {
         case 0: gpt2_matmul_tiled(o.C, o.A, (const gpt2_half *)o.W, o.bias, o.M, o.N, o.K); break;
         case 1: gpt2_matmul_int8(o.C, o.A, (const int8_t *)o.W, o.Ws, o.bias, o.M, o.N, o.K); break;
         case 2: gpt2_gemv_fp16(o.C, o.A, (const gpt2_half *)o.W, o.bias, o.N, o.K); break;
+        case 4: gpt2_attention_flash(o.C, o.A, o.M, GPT2_N_EMBD, GPT2_N_HEAD, GPT2_HEAD_DIM); break;
         default: gpt2_gemv_int8(o.C, o.A, (const int8_t *)o.W, o.Ws, o.bias, o.N, o.K); break;
     }
 }

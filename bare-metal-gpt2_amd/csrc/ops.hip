@@ -15,6 +15,7 @@
 #include "attn.h"
 
 namespace g2 {
+void attention_prefill(uint16_t *att, const uint16_t *qkv, int T);   // attn_prefill.hip
 
 // ------------------------------------------------------------------ embed
 __global__ void k_embed(uint16_t *__restrict__ x, const uint16_t *__restrict__ wte, const uint16_t *__restrict__ wpe,
@@ -128,28 +129,6 @@ __global__ void k_add8(f16x8 *__restrict__ x, const f16x8 *__restrict__ y, size_
 #pragma unroll
     for (int c = 0; c < 8; ++c) a[c] = (f16)((float)a[c] + (float)b[c]);
     x[i] = a;
-}
-
-// Prefill: grid (ceil(T/4), H), four waves = four consecutive queries of one head.
-__global__ __launch_bounds__(256) void k_attention_prefill(uint16_t *__restrict__ att, const uint16_t *__restrict__ qkv,
-                                                           int T) {
-    constexpr int E = GPT2_N_EMBD, D = GPT2_HEAD_DIM, S = 3 * GPT2_N_EMBD;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int h = blockIdx.y, i = blockIdx.x * 4 + w;
-    if (i >= T) return;
-    f16x8 q[8];
-    load_q(q, qkv + (size_t)i * S + h * D);
-    AttnState st;
-    init_state(st);
-    attend_range(q, qkv + E + h * D, qkv + 2 * E + h * D, S, 0, i + 1, 0.125f, st);
-    reduce_slots(st);
-    if (lane < 8) {
-        const float inv = 1.0f / st.l;
-        f16x8 r;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) r[e] = (f16)(st.c[e] * inv);
-        *reinterpret_cast<f16x8 *>(att + (size_t)i * E + h * D + 8 * lane) = r;
-    }
 }
 
 // Merge the NW waves' partial (m, l, c) states of one head through LDS and write the context.
@@ -394,8 +373,7 @@ extern "C" void gpt2_attention_flash(gpt2_half *att, const gpt2_half *qkv, int T
         return;
     }
     if (!att || !qkv || !aligned16(att) || !aligned16(qkv)) { arg_fail("gpt2_attention_flash: null/unaligned"); return; }
-    hipLaunchKernelGGL(k_attention_prefill, dim3(cdiv(T, 4), GPT2_N_HEAD), dim3(256), 0, stream(), att, qkv, T);
-    check_launch("k_attention_prefill");
+    attention_prefill(att, qkv, T);
 }
 
 extern "C" void gpt2_quantize_rows(int8_t *q, float *s, const gpt2_half *w, int N, int K) {

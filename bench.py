@@ -13,8 +13,10 @@ Also reported in the same JSON line:
                 48-GEMV trunk chain of one decode step, and the same kernel on the INT8 tied head
                 (38.6 MB per launch, where the launch floor no longer hides the streaming rate)
   head_gemv     fp16 tied-head GEMV (77.3 MB) cold / warm
+  attention_prefill  causal MFMA prefill attention per launch at T=512 and T=1024 (12 heads x 64)
   decode        GPT-2-124M decode tok/s @ctx=512: INT8 trunk + fp16 head, one hipGraph replay per
-                token, after a P=512 prefill; plus the mean over the 511-step greedy run
+                token, after a P=512 prefill (the prefill itself is timed too); plus the mean over
+                the 511-step greedy run
   cpu_baseline  the reference's own cpu/forward_cpu.c matmul (oracle/_ref, if built) or the oracle
                 restatement, on the same four GEMM shapes, on this host's cores
 
@@ -243,6 +245,22 @@ def bench_gemv(B):
     return res, head_res
 
 
+# ------------------------------------------------------------------------------ prefill attention
+def bench_attention(B):
+    """Causal prefill attention (gpt2_attention_flash) over qkv[T, 2304], 12 heads x 64 dims.  FLOPs
+    counted over the causal triangle: 2 (q.k) + 2 (p.v) per (query, key <= query, dim, head)."""
+    rng = np.random.default_rng(99)
+    res = {}
+    for T in (512, 1024):
+        qkv = B.dev(f16(rng, (T, 2304), 1.0))
+        att = B.empty(T * 768 * 2)
+        ms, _ = B.run_ops([B.op(4, att.ptr, qkv.ptr, None, None, None, T, 0, 0)], 20, 500)
+        fl = 4.0 * 12 * 64 * T * (T + 1) / 2
+        res[f"T{T}"] = {"us": round(ms * 1e3, 3), "gflop": round(fl / 1e9, 4),
+                        "tflops": round(fl / (ms * 1e-3) / 1e12, 2)}
+    return res
+
+
 # ------------------------------------------------------------------------------ decode (config 5)
 def bench_decode(B, steady_reps=64):
     import importlib
@@ -264,8 +282,15 @@ def bench_decode(B, steady_reps=64):
     caps = pkg.GPT2CapsGPU()
     caps.logits = logits.ptr
     caps.logits_all = 0
-    L.gpt2_prefill_fill_cache(be, C.byref(model.gpu), C.byref(kv.kv), d_ids.ptr, P, C.byref(scr.s), C.byref(caps))
-    L.gpt2_sync()
+    # the P=512 prefill itself (INT8 trunk GEMMs, attention, head row, K/V fill), host-timed per call
+    pre = []
+    for i in range(6):
+        L.gpt2_sync()
+        t = time.perf_counter()
+        L.gpt2_prefill_fill_cache(be, C.byref(model.gpu), C.byref(kv.kv), d_ids.ptr, P, C.byref(scr.s), C.byref(caps))
+        L.gpt2_sync()
+        if i >= 1:
+            pre.append((time.perf_counter() - t) * 1e3)
     pkg.check("prefill")
     first = int(np.argmax(pkg.half_bits_to_f32(logits.numpy(np.uint16, (VOCAB,)))))
     ms = C.c_float()
@@ -318,7 +343,8 @@ def bench_decode(B, steady_reps=64):
     kv_bytes = L.gpt2_kv_step_bytes(C.byref(kv.kv), P + 1)
     med = float(np.median(samples))
     med_multi = float(np.median(samples_multi))
-    res = {"step": "persistent (one kernel per token)" if mode == pkg.DECODE_PERSISTENT else "multi-kernel graph",
+    res = {"prefill_ms_at_512": round(float(np.median(pre)), 4),
+           "step": "persistent (one kernel per token)" if mode == pkg.DECODE_PERSISTENT else "multi-kernel graph",
            "tok_s_at_512": round(1000.0 / med, 1), "ms_step_at_512": round(med, 4),
            "ms_step_min_max": [round(min(samples), 4), round(max(samples), 4)],
            "multi_kernel_graph_tok_s_at_512": round(1000.0 / med_multi, 1),
@@ -416,6 +442,9 @@ def main():
         log(f"gemv: {gemv}\nhead: {head}")
         out["gemv_int8"] = gemv
         out["head_gemv_fp16"] = head
+        out["attention_prefill"] = bench_attention(B)
+        B.keep.clear()
+        log(f"attention: {out['attention_prefill']}")
         if not args.no_decode:
             out["decode"] = bench_decode(B)
             B.keep.clear()

@@ -77,7 +77,9 @@ def test_embed_exact(pkg, L):
     assert np.array_equal(back(dx, (1, E))[0], oracle.fp16_view(wte[ids[3]] + wpe[300]))
 
 
-@pytest.mark.parametrize("T", [1, 2, 63, 64, 65, 200, 512])
+# 16-query blocks and 32-key chunks: sizes on, just past and just short of those edges, and the
+# largest cache (1024 rows).
+@pytest.mark.parametrize("T", [1, 2, 15, 16, 17, 31, 32, 33, 48, 63, 64, 65, 127, 200, 512, 777, 1024])
 def test_prefill_attention(pkg, L, T):
     rng = np.random.default_rng(T)
     qkv = f16v(rng, (T, 2304), 1.0)
@@ -86,6 +88,35 @@ def test_prefill_attention(pkg, L, T):
     L.gpt2_sync()
     pkg.check("attention")
     tol_check(back(da, (T, 768)), oracle.attention(qkv))
+
+
+def test_prefill_attention_peaked_scores(pkg, L):
+    """q, k ~ N(0, 16): scores q.k/8 of std 16, softmax near one-hot per row (online rescaling)."""
+    rng = np.random.default_rng(77)
+    T = 300
+    qkv = f16v(rng, (T, 2304), 1.0)
+    qkv[:, :1536] = oracle.fp16_view(qkv[:, :1536] * np.float32(4.0))
+    dq, da = dev16(pkg, qkv), pkg.Dev(T * 768 * 2)
+    L.gpt2_attention_flash(da.ptr, dq.ptr, T, 768, 12, 64)
+    L.gpt2_sync()
+    pkg.check("attention")
+    got = back(da, (T, 768))
+    assert np.isfinite(got).all()
+    tol_check(got, oracle.attention(qkv))
+
+
+def test_prefill_attention_equal_keys_is_mean(pkg, L):
+    """All keys equal: every row is the running mean of the values (exact weights 1/(i+1))."""
+    rng = np.random.default_rng(78)
+    T = 129
+    qkv = f16v(rng, (T, 2304), 1.0)
+    qkv[:, 768:1536] = qkv[0, 768:1536]
+    dq, da = dev16(pkg, qkv), pkg.Dev(T * 768 * 2)
+    L.gpt2_attention_flash(da.ptr, dq.ptr, T, 768, 12, 64)
+    L.gpt2_sync()
+    pkg.check("attention")
+    mean = np.cumsum(qkv[:, 1536:].astype(np.float64), 0) / np.arange(1, T + 1)[:, None]
+    tol_check(back(da, (T, 768)), mean)
 
 
 def test_attention_is_causal(pkg, L):
