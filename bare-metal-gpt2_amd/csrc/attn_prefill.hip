@@ -7,7 +7,8 @@
 // Design, MI355X-first:
 //   * A work-group owns 16 queries of one head; its four waves split the keys [0, last query] in
 //     32-key chunks (chunk c on wave c % 4), each keeping its own online-softmax state, merged
-//     through LDS at the end.  The heaviest query blocks (the last ones) are dispatched first.
+//     through LDS at the end.  Work-groups are assigned XCD-aware (each XCD's L2 serves 1.5 heads),
+//     heaviest query blocks first.
 //   * Scores on v_mfma_f32_16x16x32_f16 with the keys as the A operand and the queries as B:
 //     S[key][query], so a lane holds four keys of one query (keys 4g..4g+3 of a 16-key tile, lane
 //     group g = lane / 16).  K and Q fragments are 16-byte loads straight from qkv (8 consecutive
@@ -18,9 +19,11 @@
 //     softmax, converted to fp16 in registers.  V^T (keys contiguous per dim) is the A operand: each
 //     wave transposes its chunk's 32 x 64 V block through its own LDS tile (a lane packs four keys
 //     of one dim into one 8-byte write; a fragment is two 8-byte reads).
-//   * Softmax in the log2 domain (scores pre-scaled by log2(e)/8, exp2), the row maximum shared by
-//     the lane groups of a query each chunk; the denominator sums the fp16-rounded probabilities
-//     the MFMA sees, so the output is an exact convex combination of the value rows.
+//   * Softmax in the log2 domain (p = 2^(s*log2(e)/8 - m) as one FMA and v_exp_f32), the row maximum
+//     shared by the lane groups of a query each chunk through the VALU lane swaps (no LDS
+//     permutes); the causal mask is applied only to chunks that cross the diagonal.  The
+//     denominator sums the fp16-rounded probabilities the MFMA sees, so the output is an exact
+//     convex combination of the value rows.
 #include <cmath>
 
 #include "common.h"
@@ -32,6 +35,25 @@ constexpr int AP_CK = 32;                      // keys per chunk
 constexpr int AP_W = 4;                        // waves per work-group
 constexpr int AP_RS = 2 * AP_CK + 8;           // bytes per V^T row in LDS (32 keys + 8 B pad)
 
+// 2^x on the hardware exp unit (no denormal-range fix-up: arguments here are <= 0 and a result
+// below 2^-126 may flush to zero, which is below anything an fp16 probability can hold).
+__device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Maximum over the four lane groups of a query (lanes l, l^16, l^32, l^48), on the VALU lane
+// swaps of gfx950: swapping a value with itself pairs each lane with its partner in either order.
+__device__ __forceinline__ float group_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float group_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 __global__ __launch_bounds__(64 * AP_W) void k_attn_prefill_mfma(uint16_t *__restrict__ att,
                                                                   const uint16_t *__restrict__ qkv, int T) {
     constexpr int E = GPT2_N_EMBD, D = GPT2_HEAD_DIM, S3 = 3 * GPT2_N_EMBD;
@@ -40,10 +62,26 @@ __global__ __launch_bounds__(64 * AP_W) void k_attn_prefill_mfma(uint16_t *__res
     __shared__ float mrg_m[AP_W][AP_QB], mrg_l[AP_W][AP_QB];
     __shared__ f32x4 mrg_o[AP_W][AP_W][64];    // [source wave][dim group][lane]
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // wave through readfirstlane: the chunk loop counter and the mask test are then scalar
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int jq = lane & 15, g = lane >> 4;
-    const int h = blockIdx.y;
-    const int q0 = (gridDim.x - 1 - blockIdx.x) * AP_QB;   // heaviest blocks first
+    // XCD-aware assignment (work-group b runs on XCD b % 8): XCD x takes every query block of head
+    // x and every other block of head 8 + x/2, so its L2 holds the keys and values of 1.5 heads
+    // instead of all 12.  Within an XCD the blocks go heaviest first (qi = rank from the last block).
+    const int nb = (T + AP_QB - 1) / AP_QB;
+    int h, qi;
+    {
+        const int x = blockIdx.x & 7, k = blockIdx.x >> 3, i3 = k / 3, r3 = k - 3 * i3;
+        if (r3 < 2) {
+            h = x;
+            qi = 2 * i3 + r3;
+        } else {
+            h = 8 + (x >> 1);
+            qi = 2 * i3 + (x & 1);
+        }
+    }
+    if (qi >= nb) return;                      // the grid is rounded up (whole work-group leaves)
+    const int q0 = (nb - 1 - qi) * AP_QB;
     const int qlast = min(q0 + AP_QB, T) - 1;
     const int nc = qlast / AP_CK + 1;          // chunks over keys [0, qlast]; chunk start <= q0
     const int q = q0 + jq;                     // this lane's query (q >= T: computed, not stored)
@@ -76,47 +114,48 @@ __global__ __launch_bounds__(64 * AP_W) void k_attn_prefill_mfma(uint16_t *__res
     f32x4 o[4];
 #pragma unroll
     for (int dg = 0; dg < 4; ++dg) o[dg] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // Loads are unconditional (chunk index clamped to the last one): no chunk register is ever
-    // left undefined on a path the compiler can see.
-    Chunk cur, nxt;
-    load(min(wave, nc - 1), cur);
-    for (int c = wave; c < nc; c += AP_W) {
-        load(min(c + AP_W, nc - 1), nxt);   // the next chunk of this wave (a repeat at the end)
+    // One chunk: scores, online softmax, V^T through LDS, P.V.  Two register buffers alternate
+    // (the next chunk of this wave loads while one is consumed); loads are unconditional, the
+    // chunk index clamped to the last one, so no buffer is ever undefined on a compiler-visible path.
+    auto step = [&](int c, const Chunk &R) {
         const int kc = c * AP_CK;
         // ---- scores of keys kc + 16t + 4g + r for query q
         f32x4 s[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[t][0], qf0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[t][1], qf1, s[t], 0, 0, 0);
+            s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(R.k[t][0], qf0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(R.k[t][1], qf1, s[t], 0, 0, 0);
         }
-        float x[8];
+        // Causal mask only on a chunk that reaches past the block's first query (wave-uniform test).
+        if (kc + AP_CK - 1 > q0) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (kc + 16 * t + 4 * g + r > q) s[t][r] = -INFINITY;
+        }
+        float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                         fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+        mx = group_max(mx);
+        const float mnew = fmaxf(m, mx * SL2);  // finite: key kc <= q0 <= q
+        const float corr = exp2_raw(m - mnew);  // 0 on the wave's first chunk
+        m = mnew;
+        f16x8 pb;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) x[4 * t + r] = (kc + 16 * t + 4 * g + r <= q) ? s[t][r] * SL2 : -INFINITY;
-        float mx = x[0];
-#pragma unroll
-        for (int e = 1; e < 8; ++e) mx = fmaxf(mx, x[e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mnew = fmaxf(m, mx);        // finite: key kc <= q0 <= q
-        const float corr = exp2f(m - mnew);     // 0 on the wave's first chunk
-        m = mnew;
-        f16x8 pb;
+            for (int r = 0; r < 4; ++r) pb[4 * t + r] = (f16)exp2_raw(fmaf(s[t][r], SL2, -mnew));
+        // the denominator sums exactly the fp16 probabilities the MFMA multiplies
         float ps = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            pb[e] = (f16)exp2f(x[e] - mnew);
-            ps += (float)pb[e];
-        }
-        lsum = lsum * corr + ps;
+        for (int e = 0; e < 8; e += 2) ps = __builtin_amdgcn_fdot2(f16x2{pb[e], pb[e + 1]}, f16x2{1, 1}, ps, false);
+        lsum = fmaf(lsum, corr, ps);
         // ---- V^T of the chunk into this wave's LDS tile: row d holds keys 0..31
         {
             uint32_t u[4][4];   // u[i][j]: dims vd+2j (low half), vd+2j+1 (high half) of key vk+i
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint4 b = __builtin_bit_cast(uint4, cur.v[i]);
+                const uint4 b = __builtin_bit_cast(uint4, R.v[i]);
                 u[i][0] = b.x;
                 u[i][1] = b.y;
                 u[i][2] = b.z;
@@ -145,11 +184,18 @@ __global__ __launch_bounds__(64 * AP_W) void k_attn_prefill_mfma(uint16_t *__res
             o[dg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[dg] * corr, 0, 0, 0);
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // reads done before the next chunk's writes
-        cur = nxt;
+    };
+    Chunk A, B;
+    load(min(wave, nc - 1), A);
+    for (int c = wave; c < nc; c += 2 * AP_W) {
+        load(min(c + AP_W, nc - 1), B);
+        step(c, A);
+        if (c + AP_W >= nc) break;
+        load(min(c + 2 * AP_W, nc - 1), A);
+        step(c + AP_W, B);
     }
     // ---- merge the four waves' states: wave w finishes dims 16w .. 16w+15
-    lsum += __shfl_xor(lsum, 16, 64);
-    lsum += __shfl_xor(lsum, 32, 64);
+    lsum = group_sum(lsum);
     if (g == 0) {
         mrg_m[wave][jq] = m;
         mrg_l[wave][jq] = lsum;
@@ -168,7 +214,7 @@ __global__ __launch_bounds__(64 * AP_W) void k_attn_prefill_mfma(uint16_t *__res
     float L = 0.f;
 #pragma unroll
     for (int u = 0; u < AP_W; ++u) {
-        const float f = (lw[u] != 0.f) ? exp2f(mw[u] - mmax) : 0.f;
+        const float f = (lw[u] != 0.f) ? exp2_raw(mw[u] - mmax) : 0.f;
         L += lw[u] * f;
         acc += mrg_o[u][wave][lane] * f;
     }
@@ -181,7 +227,8 @@ __global__ __launch_bounds__(64 * AP_W) void k_attn_prefill_mfma(uint16_t *__res
 }
 
 void attention_prefill(uint16_t *att, const uint16_t *qkv, int T) {
-    hipLaunchKernelGGL(k_attn_prefill_mfma, dim3(cdiv(T, AP_QB), GPT2_N_HEAD), dim3(64 * AP_W), 0, stream(), att, qkv, T);
+    static_assert(GPT2_N_HEAD == 12, "the XCD assignment covers 12 heads on 8 XCDs");
+    hipLaunchKernelGGL(k_attn_prefill_mfma, dim3(8 * 3 * cdiv(cdiv(T, AP_QB), 2)), dim3(64 * AP_W), 0, stream(), att, qkv, T);
     check_launch("k_attn_prefill_mfma");
 }
 
