@@ -18,8 +18,10 @@
 //   * Work-group -> tile mapping is XCD-aware: consecutive work-groups go round robin over the 8
 //     XCDs, so each XCD is given one contiguous run of tiles (n-major, m fastest), and the W tiles it
 //     reads stay in its own L2.
-//   * k_gemm_mfma (register-ring pipeline) takes K % 64 != 0 shapes in its predicated form; shapes
-//     or pointers no MFMA path can take (K % 8 != 0, unaligned rows) run k_gemm_generic.
+//   * k_gemm_mfma (register-ring pipeline) takes INT8 weights at the GPT-2 prefill shapes (its
+//     widening of each W fragment overlaps the next k-tiles' loads better than the LDS ring's) and
+//     K % 64 != 0 shapes in its predicated form; shapes or pointers no MFMA path can take
+//     (K % 8 != 0, unaligned rows) run k_gemm_generic.
 #include <cstdlib>
 #include <cstring>
 
@@ -525,7 +527,8 @@ static const GemmCfg kCfgs[] = {
     G2_DCFG(128, 128, 2, 4, 4),     // 6: 8 waves, wave tile 64x32
     G2_DCFG(256, 128, 4, 2, 3),     // 7: 8 waves, wave tile 64x64
     G2_DCFG(32, 32, 1, 2, 4),       // 8: 2 waves, wave tile 32x16
-    // register-ring pipeline (k_gemm_mfma), kept as a reference point for tuning
+    // register-ring pipeline (k_gemm_mfma): 10 is the INT8 pick at the GPT-2 shapes, the others
+    // are kept as reference points for tuning
     G2_CFG(96, 64, 64, 2, 2, 6),    // 9: wave tile 48x32
     G2_CFG(64, 32, 64, 2, 2, 6),    // 10: wave tile 32x16
     G2_CFG(32, 64, 64, 1, 4, 6),    // 11: wave tile 32x16
@@ -546,7 +549,7 @@ static int g_force_cfg = -2;  // -2: not read yet; -1: table
 
 static bool cfg_fits(int c, int K) { return K % kCfgs[c].kmul == 0 && K >= kCfgs[c].kmin; }
 
-static int pick_cfg(int M, int N, int K) {
+static int pick_cfg(int M, int N, int K, bool qw = false) {
     if (g_force_cfg == -2) {
         const char *e = getenv("GPT2_GEMM_CFG");
         g_force_cfg = e ? atoi(e) : -1;
@@ -557,6 +560,13 @@ static int pick_cfg(int M, int N, int K) {
     // distinct, L2-cold weights per launch on MI355X), then a fallback: the largest tile that still
     // gives about one work-group per CU (256 CUs), among the configs whose K constraint holds; -1
     // when none does (the guarded kernel runs).
+    if (M > 256 && M <= 512 && qw) {
+        // INT8 weights: the register-ring kernel with 64x32 tiles (2x2 waves, 6 k-tiles in flight)
+        // is fastest on all four shapes (QKV 9.8, attn-proj 6.0, fc 10.6, mlp-proj 14.0 us against
+        // 12.0 / 7.2 / 11.7 / 25.6 for the fp16 picks below; same sweep, same outputs).
+        const bool gpt2 = (N == 768 || N == 2304 || N == 3072) && (K == 768 || K == 3072);
+        if (gpt2 && cfg_fits(10, K)) return 10;
+    }
     if (M > 256 && M <= 512) {
         int c = -1;
         if (N == 768 && K == 768) c = 3;                  // attn-proj: 64x32, 4 waves, 4 stages
@@ -601,7 +611,7 @@ void gemm(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const 
     if ((long)M * N == 0) return;
     // K == 0 (an empty sum, C = bias or 0) falls through to the generic kernel.
     if (K > 0 && mfma_ok(A, W, K, qw)) {
-        const int c = (cfg >= 0 && cfg < kNumCfgs && cfg_fits(cfg, K)) ? cfg : pick_cfg(M, N, K);
+        const int c = (cfg >= 0 && cfg < kNumCfgs && cfg_fits(cfg, K)) ? cfg : pick_cfg(M, N, K, qw);
         if (c >= 0) launch_gemm(kCfgs[c], C, A, W, Ws, bias, M, N, K, qw);
         else launch_gemm(kGuardCfgs[(long)cdiv(N, 64) * cdiv(M, 64) >= 256 ? 0 : 1], C, A, W, Ws, bias, M, N, K, qw);
         check_launch(qw ? "k_gemm_mfma<int8>" : "k_gemm_mfma<fp16>");
