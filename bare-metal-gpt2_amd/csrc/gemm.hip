@@ -28,6 +28,8 @@
 #include "common.h"
 
 namespace g2 {
+void gemv(uint16_t *C, const uint16_t *x, const void *W, const float *Ws, const uint16_t *bias, int N, int K, bool qw,
+          int cfg);   // gemv.hip
 
 // 16-byte chunk swizzle inside an LDS row of CH chunks.  Eight consecutive rows read at one
 // logical chunk land on eight distinct 16-byte bank groups (measured: zero SQ_LDS_BANK_CONFLICT).
@@ -284,8 +286,11 @@ __device__ __forceinline__ f16x8 i8x8_to_f16x8(uint2 w) {
     return __builtin_bit_cast(f16x8, v);
 }
 
-template <int BN, int BM, int WN, int WM, int S, bool QW>
-__global__ __launch_bounds__(WN *WM * 64) void k_gemm_dl(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
+// KS > 1 splits the k-tiles inside the work-group: KS groups of WN x WM waves, each with its own LDS
+// ring, run the same pipeline over consecutive 1/KS shares of K (so their barriers line up), and
+// groups 1.. add their accumulators into group 0's through LDS before the epilogue.
+template <int BN, int BM, int WN, int WM, int S, bool QW, int KS = 1>
+__global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
                                                          const void *__restrict__ Wv, const float *__restrict__ Ws,
                                                          const uint16_t *__restrict__ bias, int M, int N, int K,
                                                          int tiles_m, int ntiles, int vec_store) {
@@ -303,11 +308,13 @@ __global__ __launch_bounds__(WN *WM * 64) void k_gemm_dl(uint16_t *__restrict__ 
     static_assert(TN * 16 == WTN && TM * 16 == WTM, "wave tile is whole 16x16 blocks");
     static_assert(S >= 2 && (S - 2) * LMAX < 64, "stages");
 
-    __shared__ __attribute__((aligned(1024))) char smem[S * STAGE];
+    __shared__ __attribute__((aligned(1024))) char smem_all[KS * S * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nk = K / BK;
+    const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kg = wave_all / NW, wave = wave_all % NW;   // k group; wave inside the group
+    char *smem = smem_all + kg * S * STAGE;
+    const int nk = K / BK / KS;                           // k-tiles per group
     const size_t welt = QW ? 1 : 2;
     const int tile = xcd_tile(blockIdx.x, ntiles);
     const int n0 = (tile / tiles_m) * BN, m0 = (tile % tiles_m) * BM;
@@ -336,6 +343,8 @@ __global__ __launch_bounds__(WN *WM * 64) void k_gemm_dl(uint16_t *__restrict__ 
             kstep[j] = BK * (int)welt;
         }
     }
+#pragma unroll
+    for (int j = 0; j < LMAX; ++j) gsrc[j] += (size_t)kg * nk * kstep[j];   // this group's share of K
     const int nld = (REM == 0 || wave < REM) ? LMAX : LO;   // wave-uniform
     auto issue = [&](int kt) {
         char *st = smem + (kt % S) * STAGE;
@@ -422,7 +431,83 @@ __global__ __launch_bounds__(WN *WM * 64) void k_gemm_dl(uint16_t *__restrict__ 
         mfmas(F);
     }
 
+    if constexpr (KS > 1) {
+        // Groups 1.. hand their partial sums to group 0 through the (now idle) LDS rings.
+        constexpr int NACC = TN * TM * 4;
+        static_assert((KS - 1) * NW * NACC * 64 * 4 <= KS * S * STAGE, "reduction buffer fits the rings");
+        float *red = reinterpret_cast<float *>(smem_all);
+        lds_barrier();   // every group is done with its ring
+        if (kg > 0) {
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+                for (int b = 0; b < TM; ++b)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        red[(((kg - 1) * NW + wave) * NACC + (a * TM + b) * 4 + i) * 64 + lane] = acc[a][b][i];
+        }
+        lds_barrier();
+        if (kg == 0) {
+#pragma unroll
+            for (int g = 1; g < KS; ++g)
+#pragma unroll
+                for (int a = 0; a < TN; ++a)
+#pragma unroll
+                    for (int b = 0; b < TM; ++b)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            acc[a][b][i] += red[(((g - 1) * NW + wave) * NACC + (a * TM + b) * 4 + i) * 64 + lane];
+        }
+    }
     // Epilogue: lane holds D[n][m] for n = nb..nb+3, m = mrow.
+    if (!vec_store) {
+        // Rows of C that are not 8-byte aligned (odd N: the tied head's 50257 columns): the tile
+        // is staged in the now idle LDS ring and leaves row by row, a wave writing 64 consecutive
+        // column pairs per store (dword-aligned in C; a lone first or last column as a 2-byte
+        // store), instead of 2-byte stores scattered over 16 rows per instruction.
+        constexpr int CS = BN + 4;   // staged row stride (halves): rows 8 bytes apart in banks
+        static_assert(BM * CS * 2 <= KS * S * STAGE, "staged C tile fits the LDS ring");
+        uint16_t *ct = reinterpret_cast<uint16_t *>(smem_all);
+        lds_barrier();   // every wave is done with the last k-tile's fragments (and the k-group sums)
+#pragma unroll
+        for (int a = 0; a < TN && kg == 0; ++a) {
+            const int nl = wn0 + a * 16 + lgrp * 4, nb = n0 + nl;
+            float sc[4] = {1.f, 1.f, 1.f, 1.f}, bs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (nb + i < N) {
+                    if constexpr (QW) sc[i] = Ws[nb + i];
+                    if (bias) bs[i] = h2f(bias[nb + i]);
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < TM; ++b) {
+                const int ml = wm0 + b * 16 + lrow;
+                uint16_t o[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float v = acc[a][b][i];
+                    if constexpr (QW) v = v * sc[i];
+                    o[i] = f2h(v + bs[i]);
+                }
+                *reinterpret_cast<uint2 *>(ct + ml * CS + nl) =
+                    uint2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+            }
+        }
+        lds_barrier();
+        const int ncols = min(BN, N - n0);
+        for (int r = wave_all; r < BM && m0 + r < M; r += NW * KS) {
+            const uint16_t *src = ct + r * CS;
+            uint16_t *dst = C + (size_t)(m0 + r) * N + n0;
+            const int head = (int)(((uintptr_t)dst >> 1) & 1);   // column 0 is not 4-byte aligned
+            for (int c = head + 2 * lane; c + 1 < ncols; c += 128)
+                *reinterpret_cast<uint32_t *>(dst + c) = (uint32_t)src[c] | ((uint32_t)src[c + 1] << 16);
+            if (lane == 0 && head) dst[0] = src[0];
+            if (lane == 1 && ((ncols - head) & 1)) dst[ncols - 1] = src[ncols - 1];
+        }
+        return;
+    }
+    if (kg != 0) return;
 #pragma unroll
     for (int a = 0; a < TN; ++a) {
         const int nb = n0 + wn0 + a * 16 + lgrp * 4;
@@ -513,26 +598,42 @@ struct GemmCfg {
 #define G2_CFG(BN, BM, BK, WN, WM, D) \
     {BN, BM, BK * D, 0, 256, k_gemm_mfma<BN, BM, BK, WN, WM, false, D>, k_gemm_mfma<BN, BM, BK, WN, WM, true, D>, \
      "bn" #BN "_bm" #BM "_bk" #BK "_w" #WN "x" #WM "_d" #D}
-// Direct-to-LDS pipeline: K % 64 == 0 and at least S-1 k-tiles.
+// Direct-to-LDS pipeline: K % 64 == 0 and at least S-1 k-tiles (per k group: K % (64 KS) == 0).
 #define G2_DCFG(BN, BM, WN, WM, S) \
     {BN, BM, 64, 64 * (S - 1), 64 * WN * WM, k_gemm_dl<BN, BM, WN, WM, S, false>, k_gemm_dl<BN, BM, WN, WM, S, true>, \
      "dl_bn" #BN "_bm" #BM "_w" #WN "x" #WM "_s" #S}
+#define G2_DCFGK(BN, BM, WN, WM, S, KS) \
+    {BN, BM, 64 * KS, 64 * KS * (S - 1), 64 * WN * WM * KS, k_gemm_dl<BN, BM, WN, WM, S, false, KS>, \
+     k_gemm_dl<BN, BM, WN, WM, S, true, KS>, "dl_bn" #BN "_bm" #BM "_w" #WN "x" #WM "_s" #S "_k" #KS}
 static const GemmCfg kCfgs[] = {
-    G2_DCFG(96, 64, 2, 4, 4),       // 0: 8 waves, wave tile 48x16 (QKV)
-    G2_DCFG(128, 64, 4, 2, 3),      // 1: 8 waves, wave tile 32x32 (fc)
-    G2_DCFG(32, 64, 1, 4, 4),       // 2: 4 waves, wave tile 32x16 (attn-proj, mlp-proj)
+    G2_DCFG(96, 64, 2, 4, 4),       // 0: 8 waves, wave tile 48x16
+    G2_DCFG(128, 64, 4, 2, 3),      // 1: 8 waves, wave tile 32x32
+    G2_DCFG(32, 64, 1, 4, 4),       // 2: 4 waves, wave tile 32x16
     G2_DCFG(64, 32, 2, 2, 4),       // 3: 4 waves, wave tile 32x16
     G2_DCFG(96, 64, 2, 2, 6),       // 4: 4 waves, wave tile 48x32
     G2_DCFG(64, 64, 2, 4, 4),       // 5: 8 waves, wave tile 32x16
     G2_DCFG(128, 128, 2, 4, 4),     // 6: 8 waves, wave tile 64x32
     G2_DCFG(256, 128, 4, 2, 3),     // 7: 8 waves, wave tile 64x64
     G2_DCFG(32, 32, 1, 2, 4),       // 8: 2 waves, wave tile 32x16
-    // register-ring pipeline (k_gemm_mfma): 10 is the INT8 pick at the GPT-2 shapes, the others
+    G2_DCFG(48, 32, 3, 2, 4),       // 9: 6 waves, wave tile 16x16 (QKV)
+    G2_DCFG(48, 32, 1, 2, 4),       // 10: 2 waves, wave tile 48x16
+    G2_DCFG(48, 32, 3, 2, 6),       // 11: 6 waves, wave tile 16x16, 6 stages
+    G2_DCFGK(32, 64, 1, 4, 4, 2),   // 12: two k groups of 4 waves (K=3072: 24 k-tiles each)
+    G2_DCFGK(32, 32, 1, 2, 4, 2),   // 13: two k groups of 2 waves
+    G2_DCFGK(32, 32, 1, 2, 4, 4),   // 14: four k groups of 2 waves
+    G2_DCFGK(48, 32, 3, 2, 4, 2),   // 15: two k groups of 6 waves (attn-proj, mlp-proj)
+    G2_DCFGK(32, 64, 1, 4, 4, 3),   // 16: three k groups of 4 waves
+    G2_DCFGK(64, 32, 2, 2, 4, 2),   // 17: two k groups of 4 waves
+    G2_DCFGK(32, 64, 1, 4, 3, 2),   // 18: two k groups of 4 waves, 3 stages
+    G2_DCFG(96, 32, 3, 2, 4),       // 19: 6 waves, wave tile 32x16
+    G2_DCFG(48, 64, 3, 4, 4),       // 20: 12 waves, wave tile 16x16 (fc)
+    G2_DCFGK(128, 64, 4, 2, 3, 2),  // 21: two k groups of 8 waves
+    // register-ring pipeline (k_gemm_mfma): 23 is the INT8 pick at the GPT-2 shapes, the others
     // are kept as reference points for tuning
-    G2_CFG(96, 64, 64, 2, 2, 6),    // 9: wave tile 48x32
-    G2_CFG(64, 32, 64, 2, 2, 6),    // 10: wave tile 32x16
-    G2_CFG(32, 64, 64, 1, 4, 6),    // 11: wave tile 32x16
-    G2_CFG(128, 128, 64, 2, 2, 2),  // 12: wave tile 64x64
+    G2_CFG(96, 64, 64, 2, 2, 6),    // 22: wave tile 48x32
+    G2_CFG(64, 32, 64, 2, 2, 6),    // 23: wave tile 32x16
+    G2_CFG(32, 64, 64, 1, 4, 6),    // 24: wave tile 32x16
+    G2_CFG(128, 128, 64, 2, 2, 2),  // 25: wave tile 64x64
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
 
@@ -549,30 +650,38 @@ static int g_force_cfg = -2;  // -2: not read yet; -1: table
 
 static bool cfg_fits(int c, int K) { return K % kCfgs[c].kmul == 0 && K >= kCfgs[c].kmin; }
 
-static int pick_cfg(int M, int N, int K, bool qw = false) {
+// The config forced by gpt2_tune_gemm_force or the GPT2_GEMM_CFG environment variable, or -1.
+static int forced_cfg() {
     if (g_force_cfg == -2) {
         const char *e = getenv("GPT2_GEMM_CFG");
         g_force_cfg = e ? atoi(e) : -1;
         if (g_force_cfg >= kNumCfgs) g_force_cfg = -1;
     }
-    if (g_force_cfg >= 0 && cfg_fits(g_force_cfg, K)) return g_force_cfg;
+    return g_force_cfg;
+}
+
+static int pick_cfg(int M, int N, int K, bool qw = false) {
+    if (forced_cfg() >= 0 && cfg_fits(g_force_cfg, K)) return g_force_cfg;
     // Measured picks for the GPT-2 prefill shapes at M in (256, 512] (12-layer sweeps with
     // distinct, L2-cold weights per launch on MI355X), then a fallback: the largest tile that still
     // gives about one work-group per CU (256 CUs), among the configs whose K constraint holds; -1
     // when none does (the guarded kernel runs).
     if (M > 256 && M <= 512 && qw) {
-        // INT8 weights: the register-ring kernel with 64x32 tiles (2x2 waves, 6 k-tiles in flight)
-        // is fastest on all four shapes (QKV 9.8, attn-proj 6.0, fc 10.6, mlp-proj 14.0 us against
-        // 12.0 / 7.2 / 11.7 / 25.6 for the fp16 picks below; same sweep, same outputs).
-        const bool gpt2 = (N == 768 || N == 2304 || N == 3072) && (K == 768 || K == 3072);
-        if (gpt2 && cfg_fits(10, K)) return 10;
+        // INT8 weights (widened to fp16 as fragments are read): QKV and attn-proj as fp16 (9.4 and
+        // 5.4 us); fc and mlp-proj on the register-ring kernel with 64x32 tiles and 6 k-tiles in
+        // flight (10.0 and 13.7 us; the LDS-ring configs measured 10.3 and 14.6).
+        int c = -1;
+        if (N == 2304 && K == 768) c = 9;
+        else if (N == 768 && K == 768) c = 15;
+        else if ((N == 3072 && K == 768) || (N == 768 && K == 3072)) c = 23;
+        if (c >= 0 && cfg_fits(c, K)) return c;
     }
     if (M > 256 && M <= 512) {
         int c = -1;
-        if (N == 768 && K == 768) c = 3;                  // attn-proj: 64x32, 4 waves, 4 stages
-        else if (N == 768 && K == 3072) c = 2;            // mlp-proj: 32x64, 4 waves, 4 stages
-        else if (N == 2304 && K == 768) c = 0;            // QKV: 96x64, 8 waves, 4 stages
-        else if (N == 3072 && K == 768) c = 1;            // fc: 128x64, 8 waves, 3 stages
+        if (N == 768 && K == 768) c = 15;                 // attn-proj: 48x32, 2 k groups of 6 waves
+        else if (N == 768 && K == 3072) c = 15;           // mlp-proj: 48x32, 2 k groups of 6 waves
+        else if (N == 2304 && K == 768) c = 9;            // QKV: 48x32, 6 waves, 4 stages
+        else if (N == 3072 && K == 768) c = 20;           // fc: 48x64, 12 waves, 4 stages
         if (c >= 0 && cfg_fits(c, K)) return c;
     }
     const int order[] = {6, 0, 5, 2, 3, 8};
@@ -609,6 +718,12 @@ static bool gemm_args(const char *who, const void *C, const void *A, const void 
 void gemm(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const uint16_t *bias, int M, int N, int K,
           bool qw, int cfg) {
     if ((long)M * N == 0) return;
+    // M = 1 (the prefill's last-row head, a decode-shaped call) is a GEMV: the tiles would compute
+    // 128 rows and keep one.  Tuning runs that force a tile config keep the GEMM.
+    if (M == 1 && K > 0 && cfg < 0 && forced_cfg() < 0) {
+        gemv(C, A, W, Ws, bias, N, K, qw, -1);
+        return;
+    }
     // K == 0 (an empty sum, C = bias or 0) falls through to the generic kernel.
     if (K > 0 && mfma_ok(A, W, K, qw)) {
         const int c = (cfg >= 0 && cfg < kNumCfgs && cfg_fits(cfg, K)) ? cfg : pick_cfg(M, N, K, qw);

@@ -13,6 +13,8 @@ Also reported in the same JSON line:
                 48-GEMV trunk chain of one decode step, and the same kernel on the INT8 tied head
                 (38.6 MB per launch, where the launch floor no longer hides the streaming rate)
   head_gemv     fp16 tied-head GEMV (77.3 MB) cold / warm
+  gemm_int8_set the same P=512 trunk set with INT8 weights (the config-5 prefill GEMMs)
+  head_gemm     the tied head as a prefill GEMM, [512x768] . [768x50257]^T (39.5 GFLOP)
   attention_prefill  causal MFMA prefill attention per launch at T=512 and T=1024 (12 heads x 64)
   decode        GPT-2-124M decode tok/s @ctx=512: INT8 trunk + fp16 head, one hipGraph replay per
                 token, after a P=512 prefill (the prefill itself is timed too); plus the mean over
@@ -140,9 +142,10 @@ def measured_traffic(cfg_name, shapes):
            (768, 3072): "mlp-proj 512x768x3072"}
     want = [prof["per_shape"].get(key.get((x["N"], x["K"]), ""), {}) for x in shapes]
     import re
-    m = re.fullmatch(r"dl_bn(\d+)_bm(\d+)_w(\d+)x(\d+)_s(\d+)", cfg_name)
+    m = re.fullmatch(r"dl_bn(\d+)_bm(\d+)_w(\d+)x(\d+)_s(\d+)(?:_k(\d+))?", cfg_name)
     if m:
-        tag = "k_gemm_dl<{}, {}, {}, {}, {}, false>".format(*m.groups())
+        g = m.groups()
+        tag = "k_gemm_dl<{}, {}, {}, {}, {}, false, {}>".format(*g[:5], g[5] or 1)
     else:
         m = re.fullmatch(r"bn(\d+)_bm(\d+)_bk(\d+)_w(\d+)x(\d+)_d(\d+)", cfg_name)
         if not m:
@@ -243,6 +246,46 @@ def bench_gemv(B):
                 "warm_GBs": round(algo / (ms_warm * 1e-3) / 1e9, 1)}
     big.free()
     return res, head_res
+
+
+# ------------------------------------------------------------------------------ INT8 GEMM set, head GEMM
+def bench_gemm_extra(B, steps):
+    """The same P=512 trunk set with INT8 weights (gpt2_matmul_int8, the config-5 prefill path), and
+    the tied head as a prefill GEMM: [512x768] . [768x50257]^T (config 4, logits for every row)."""
+    rng = np.random.default_rng(4242)
+    L = B.L
+    X = B.dev(f16(rng, (M_PREFILL, 768), 1.0))
+    Xf = B.dev(f16(rng, (M_PREFILL, 3072), 1.0))
+    outs = {name: B.empty(M_PREFILL * N * 2) for name, N, K in GEMM_SET}
+    ops = []
+    for layer in range(N_LAYER):
+        for name, N, K in GEMM_SET:
+            q = B.dev(rng.integers(-127, 128, (N, K), dtype=np.int8))
+            s = B.dev((rng.random(N, dtype=np.float32) * np.float32(2e-4) + np.float32(1e-4)).astype(np.float32))
+            b = B.dev(f16(rng, N, 0.01))
+            ops.append(B.op(1, outs[name].ptr, (Xf if K == 3072 else X).ptr, q.ptr, s.ptr, b.ptr, M_PREFILL, N, K))
+    flops = sum(2.0 * M_PREFILL * N * K for _, N, K in GEMM_SET) * N_LAYER
+    ms, _ = B.run_ops(ops, 5, max(20, steps // 2))
+    per = []
+    for j, (name, N, K) in enumerate(GEMM_SET):
+        ms_shape, _ = B.run_ops(ops[j::4], 3, max(20, steps // 4))
+        us = ms_shape / N_LAYER * 1e3
+        per.append({"gemm": name, "us": round(us, 3), "tflops": round(2.0 * M_PREFILL * N * K / (us * 1e-6) / 1e12, 2)})
+    int8 = {"us_per_step": round(ms * 1e3, 2), "tflops": round(flops / (ms * 1e-3) / 1e12, 2), "shapes": per}
+    B.keep.clear()
+    # head GEMM: fp16 wte [50257, 768], A = 512 LayerNorm-like rows, no bias
+    N, K = VOCAB, 768
+    A = B.dev(f16(rng, (M_PREFILL, K), 1.0))
+    W = B.dev(f16(rng, (N, K), 0.02))
+    Cm = B.empty(M_PREFILL * N * 2)
+    ms_h, _ = B.run_ops([B.op(0, Cm.ptr, A.ptr, W.ptr, None, None, M_PREFILL, N, K)], 3, 50)
+    fl = 2.0 * M_PREFILL * N * K
+    achieved = fl / (ms_h * 1e-3) / 1e12
+    head = {"M": M_PREFILL, "N": N, "K": K, "gflop": round(fl / 1e9, 3), "us": round(ms_h * 1e3, 2),
+            "tflops": round(achieved, 1), "frac_of_peak": round(achieved / PEAK_FP16_TFLOPS, 4),
+            "kernel": L.gpt2_tune_gemm_name(L.gpt2_tune_gemm_pick(M_PREFILL, N, K)).decode()}
+    B.keep.clear()
+    return int8, head
 
 
 # ------------------------------------------------------------------------------ prefill attention
@@ -442,6 +485,8 @@ def main():
         log(f"gemv: {gemv}\nhead: {head}")
         out["gemv_int8"] = gemv
         out["head_gemv_fp16"] = head
+        out["gemm_int8_set"], out["head_gemm_fp16"] = bench_gemm_extra(B, args.steps)
+        log(f"int8 gemm set: {out['gemm_int8_set']}\nhead gemm: {out['head_gemm_fp16']}")
         out["attention_prefill"] = bench_attention(B)
         B.keep.clear()
         log(f"attention: {out['attention_prefill']}")

@@ -77,6 +77,34 @@ def test_int8_config_shapes(pkg, L, M, N, K):
     tol_check(got, oracle.matmul(A, oracle.dequantize(q, s), b))
 
 
+@pytest.mark.parametrize("kind", ["fp16", "int8"])
+@pytest.mark.parametrize("M,N,K", [(300, 777, 768), (129, 257, 256), (64, 1001, 192), (512, 2305, 768)])
+def test_unaligned_c_rows(pkg, L, kind, M, N, K):
+    """Odd N (rows of C not 8-byte aligned) with C itself offset by 0, 1 or 3 elements: the tile is
+    staged through LDS and written as dword column pairs plus lone end columns; the elements right
+    before and after C must stay untouched."""
+    rng = np.random.default_rng(M + N + K)
+    A, W, b = f16v(rng, (M, K), 1.0), f16v(rng, (N, K), 0.02), f16v(rng, N, 0.01)
+    q, s, _ = oracle.quantize_fp16_view(W)
+    ref = oracle.matmul(A, oracle.dequantize(q, s), b) if kind == "int8" else oracle.matmul(A, W, b)
+    dA, db = dev16(pkg, A), dev16(pkg, b)
+    dW = pkg.Dev.from_numpy(q) if kind == "int8" else dev16(pkg, W)
+    ds = pkg.Dev.from_numpy(s)
+    for off in (0, 1, 3):
+        sentinel = np.full(M * N + off + 4, 0x7BFF, np.uint16)          # fp16 65504
+        dC = pkg.Dev.from_numpy(sentinel)
+        cptr = dC.at(2 * off)
+        if kind == "int8":
+            L.gpt2_matmul_int8(cptr, dA.ptr, dW.ptr, ds.ptr, db.ptr, M, N, K)
+        else:
+            L.gpt2_matmul_tiled(cptr, dA.ptr, dW.ptr, db.ptr, M, N, K)
+        L.gpt2_sync()
+        pkg.check("gemm unaligned C")
+        out = dC.numpy(np.uint16, (M * N + off + 4,))
+        assert (out[:off] == 0x7BFF).all() and (out[off + M * N:] == 0x7BFF).all(), off
+        tol_check(oracle.f16_to_f32(out[off:off + M * N].reshape(M, N)), ref)
+
+
 def test_head_gemm_tail_columns(pkg, L):
     """Tied head at M=512: N = 50257 is odd (rows of C are 100514 B, not 16-B aligned)."""
     rng = np.random.default_rng(4)
