@@ -289,7 +289,9 @@ __device__ __forceinline__ f16x8 i8x8_to_f16x8(uint2 w) {
 // KS > 1 splits the k-tiles inside the work-group: KS groups of WN x WM waves, each with its own LDS
 // ring, run the same pipeline over consecutive 1/KS shares of K (so their barriers line up), and
 // groups 1.. add their accumulators into group 0's through LDS before the epilogue.
-template <int BN, int BM, int WN, int WM, int S, bool QW, int KS = 1>
+// U > 1 covers U consecutive k-tiles per barrier: their fragments are read back to back (one LDS
+// round trip) and then multiplied, and U tiles are refilled at a time (S % U == 0, S >= 2U).
+template <int BN, int BM, int WN, int WM, int S, bool QW, int KS = 1, int U = 1>
 __global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
                                                          const void *__restrict__ Wv, const float *__restrict__ Ws,
                                                          const uint16_t *__restrict__ bias, int M, int N, int K,
@@ -307,6 +309,7 @@ __global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restri
     constexpr int WTN = BN / WN, WTM = BM / WM, TN = WTN / 16, TM = WTM / 16;
     static_assert(TN * 16 == WTN && TM * 16 == WTM, "wave tile is whole 16x16 blocks");
     static_assert(S >= 2 && (S - 2) * LMAX < 64, "stages");
+    static_assert(U >= 1 && S % U == 0 && S >= 2 * U, "k-tiles per barrier");
 
     __shared__ __attribute__((aligned(1024))) char smem_all[KS * S * STAGE];
 
@@ -411,24 +414,29 @@ __global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restri
             }
     };
 
-    // Prologue: tiles 0 .. S-2 in flight (the config table requires nk >= S - 1).
+    // Prologue: tiles 0 .. S-U-1 in flight (the config table requires nk >= S - U, nk % U == 0).
 #pragma unroll
-    for (int s = 0; s < S - 1; ++s) issue(s);
+    for (int s = 0; s < S - U; ++s) issue(s);
     int kt = 0;
-    for (; kt + S - 1 < nk; ++kt) {
-        wait_for(S - 2);
+    for (; kt + S - U < nk; kt += U) {
+        wait_for(S - 2 * U);   // tiles kt .. kt+U-1 have landed (this wave's part; the barrier: all)
         lds_barrier();
-        issue(kt + S - 1);
-        Frag F;
-        load_frags(kt, F);
-        mfmas(F);
+#pragma unroll
+        for (int u = 0; u < U; ++u) issue(kt + S - U + u);   // into the buffers of tiles kt-U .. kt-1
+        Frag F[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) load_frags(kt + u, F[u]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) mfmas(F[u]);
     }
-    for (; kt < nk; ++kt) {
-        wait_for(nk - 1 - kt);
+    for (; kt < nk; kt += U) {
+        wait_for(nk - U - kt);
         lds_barrier();
-        Frag F;
-        load_frags(kt, F);
-        mfmas(F);
+        Frag F[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) load_frags(kt + u, F[u]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) mfmas(F[u]);
     }
 
     if constexpr (KS > 1) {
@@ -605,6 +613,10 @@ struct GemmCfg {
 #define G2_DCFGK(BN, BM, WN, WM, S, KS) \
     {BN, BM, 64 * KS, 64 * KS * (S - 1), 64 * WN * WM * KS, k_gemm_dl<BN, BM, WN, WM, S, false, KS>, \
      k_gemm_dl<BN, BM, WN, WM, S, true, KS>, "dl_bn" #BN "_bm" #BM "_w" #WN "x" #WM "_s" #S "_k" #KS}
+// ... and U k-tiles per barrier: K % (64 KS U) == 0, at least S-U k-tiles per group.
+#define G2_DCFGU(BN, BM, WN, WM, S, KS, U) \
+    {BN, BM, 64 * KS * U, 64 * KS * (S - U), 64 * WN * WM * KS, k_gemm_dl<BN, BM, WN, WM, S, false, KS, U>, \
+     k_gemm_dl<BN, BM, WN, WM, S, true, KS, U>, "dl_bn" #BN "_bm" #BM "_w" #WN "x" #WM "_s" #S "_k" #KS "_u" #U}
 static const GemmCfg kCfgs[] = {
     G2_DCFG(96, 64, 2, 4, 4),       // 0: 8 waves, wave tile 48x16
     G2_DCFG(128, 64, 4, 2, 3),      // 1: 8 waves, wave tile 32x32
@@ -615,27 +627,39 @@ static const GemmCfg kCfgs[] = {
     G2_DCFG(128, 128, 2, 4, 4),     // 6: 8 waves, wave tile 64x32
     G2_DCFG(256, 128, 4, 2, 3),     // 7: 8 waves, wave tile 64x64
     G2_DCFG(32, 32, 1, 2, 4),       // 8: 2 waves, wave tile 32x16
-    G2_DCFG(48, 32, 3, 2, 4),       // 9: 6 waves, wave tile 16x16 (QKV)
+    G2_DCFG(48, 32, 3, 2, 4),       // 9: 6 waves, wave tile 16x16
     G2_DCFG(48, 32, 1, 2, 4),       // 10: 2 waves, wave tile 48x16
     G2_DCFG(48, 32, 3, 2, 6),       // 11: 6 waves, wave tile 16x16, 6 stages
     G2_DCFGK(32, 64, 1, 4, 4, 2),   // 12: two k groups of 4 waves (K=3072: 24 k-tiles each)
     G2_DCFGK(32, 32, 1, 2, 4, 2),   // 13: two k groups of 2 waves
     G2_DCFGK(32, 32, 1, 2, 4, 4),   // 14: four k groups of 2 waves
-    G2_DCFGK(48, 32, 3, 2, 4, 2),   // 15: two k groups of 6 waves (attn-proj, mlp-proj)
+    G2_DCFGK(48, 32, 3, 2, 4, 2),   // 15: two k groups of 6 waves
     G2_DCFGK(32, 64, 1, 4, 4, 3),   // 16: three k groups of 4 waves
     G2_DCFGK(64, 32, 2, 2, 4, 2),   // 17: two k groups of 4 waves
     G2_DCFGK(32, 64, 1, 4, 3, 2),   // 18: two k groups of 4 waves, 3 stages
     G2_DCFG(96, 32, 3, 2, 4),       // 19: 6 waves, wave tile 32x16
-    G2_DCFG(48, 64, 3, 4, 4),       // 20: 12 waves, wave tile 16x16 (fc)
+    G2_DCFG(48, 64, 3, 4, 4),       // 20: 12 waves, wave tile 16x16
     G2_DCFGK(128, 64, 4, 2, 3, 2),  // 21: two k groups of 8 waves
-    // register-ring pipeline (k_gemm_mfma): 23 is the INT8 pick at the GPT-2 shapes, the others
-    // are kept as reference points for tuning
-    G2_CFG(96, 64, 64, 2, 2, 6),    // 22: wave tile 48x32
-    G2_CFG(64, 32, 64, 2, 2, 6),    // 23: wave tile 32x16
-    G2_CFG(32, 64, 64, 1, 4, 6),    // 24: wave tile 32x16
-    G2_CFG(128, 128, 64, 2, 2, 2),  // 25: wave tile 64x64
+    G2_DCFGU(48, 32, 3, 2, 4, 2, 2),  // 22: as 15, two k-tiles per barrier
+    G2_DCFGU(48, 32, 3, 2, 6, 2, 2),  // 23: as 15, two k-tiles per barrier, 6 stages (mlp-proj)
+    G2_DCFGU(48, 32, 3, 2, 4, 1, 2),  // 24: as 9, two k-tiles per barrier (QKV)
+    G2_DCFGU(48, 32, 3, 2, 6, 1, 2),  // 25: as 9, two k-tiles per barrier, 6 stages
+    G2_DCFGU(48, 64, 3, 4, 4, 1, 2),  // 26: as 20, two k-tiles per barrier (fc)
+    G2_DCFGU(48, 64, 3, 4, 6, 1, 2),  // 27: as 20, two k-tiles per barrier, 6 stages
+    G2_DCFGU(48, 32, 3, 2, 6, 1, 3),  // 28: as 9, three k-tiles per barrier
+    G2_DCFGU(48, 64, 3, 4, 6, 1, 3),  // 29: as 20, three k-tiles per barrier
+    G2_DCFGU(48, 32, 3, 2, 6, 2, 3),  // 30: as 15, three k-tiles per barrier
+    G2_DCFGU(48, 32, 3, 2, 8, 1, 4),  // 31: as 9, four k-tiles per barrier (attn-proj)
+    G2_DCFGU(48, 64, 3, 4, 8, 1, 4),  // 32: as 20, four k-tiles per barrier
+    G2_DCFGU(48, 32, 3, 2, 8, 2, 4),  // 33: as 15, four k-tiles per barrier (160 KB of LDS; INT8 mlp-proj)
+    // register-ring pipeline (k_gemm_mfma): reference points for tuning
+    G2_CFG(96, 64, 64, 2, 2, 6),    // 34: wave tile 48x32
+    G2_CFG(64, 32, 64, 2, 2, 6),    // 35: wave tile 32x16
+    G2_CFG(32, 64, 64, 1, 4, 6),    // 36: wave tile 32x16
+    G2_CFG(128, 128, 64, 2, 2, 2),  // 37: wave tile 64x64
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
+static_assert(sizeof(kCfgs) / sizeof(kCfgs[0]) == 38, "the pick table names configs by index");
 
 // Any K % 8 == 0 (int8: K % 16 == 0): predicated loads, one k-tile of prefetch.
 #define G2_GCFG(BN, BM, WN, WM) \
@@ -662,26 +686,28 @@ static int forced_cfg() {
 
 static int pick_cfg(int M, int N, int K, bool qw = false) {
     if (forced_cfg() >= 0 && cfg_fits(g_force_cfg, K)) return g_force_cfg;
-    // Measured picks for the GPT-2 prefill shapes at M in (256, 512] (12-layer sweeps with
-    // distinct, L2-cold weights per launch on MI355X), then a fallback: the largest tile that still
+    // Measured picks for the GPT-2 prefill shapes at M in (256, 512]: a grid over per-shape configs
+    // timed as the whole step (12 layers x {QKV, attn-proj, fc, mlp-proj}, distinct weights, back to
+    // back on MI355X; a kernel's best config alone and inside the step differ, attn-proj most),
+    // then a fallback: the largest tile that still
     // gives about one work-group per CU (256 CUs), among the configs whose K constraint holds; -1
     // when none does (the guarded kernel runs).
     if (M > 256 && M <= 512 && qw) {
-        // INT8 weights (widened to fp16 as fragments are read): QKV and attn-proj as fp16 (9.4 and
-        // 5.4 us); fc and mlp-proj on the register-ring kernel with 64x32 tiles and 6 k-tiles in
-        // flight (10.0 and 13.7 us; the LDS-ring configs measured 10.3 and 14.6).
+        // INT8 weights (widened to fp16 as fragments are read), picked the same way: 421.5 us per
+        // 12-layer step against 467.3 with the fp16 picks of the previous table.
         int c = -1;
-        if (N == 2304 && K == 768) c = 9;
-        else if (N == 768 && K == 768) c = 15;
-        else if ((N == 3072 && K == 768) || (N == 768 && K == 3072)) c = 23;
+        if (N == 2304 && K == 768) c = 24;                // QKV: 48x32, 6 waves, 2 k-tiles/barrier
+        else if (N == 768 && K == 768) c = 31;            // attn-proj: 48x32, 8 stages, 4/barrier
+        else if (N == 3072 && K == 768) c = 26;           // fc: 48x64, 12 waves, 2/barrier
+        else if (N == 768 && K == 3072) c = 33;           // mlp-proj: 48x32, 2 k groups, 8 stages, 4/barrier
         if (c >= 0 && cfg_fits(c, K)) return c;
     }
     if (M > 256 && M <= 512) {
         int c = -1;
-        if (N == 768 && K == 768) c = 15;                 // attn-proj: 48x32, 2 k groups of 6 waves
-        else if (N == 768 && K == 3072) c = 15;           // mlp-proj: 48x32, 2 k groups of 6 waves
-        else if (N == 2304 && K == 768) c = 9;            // QKV: 48x32, 6 waves, 4 stages
-        else if (N == 3072 && K == 768) c = 20;           // fc: 48x64, 12 waves, 4 stages
+        if (N == 768 && K == 768) c = 31;                 // attn-proj: 48x32, 6 waves, 8 stages, 4/barrier
+        else if (N == 768 && K == 3072) c = 23;           // mlp-proj: 48x32, 2 k groups, 6 stages, 2/barrier
+        else if (N == 2304 && K == 768) c = 24;           // QKV: 48x32, 6 waves, 2 k-tiles/barrier
+        else if (N == 3072 && K == 768) c = 26;           // fc: 48x64, 12 waves, 2 k-tiles/barrier
         if (c >= 0 && cfg_fits(c, K)) return c;
     }
     const int order[] = {6, 0, 5, 2, 3, 8};

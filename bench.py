@@ -142,10 +142,10 @@ def measured_traffic(cfg_name, shapes):
            (768, 3072): "mlp-proj 512x768x3072"}
     want = [prof["per_shape"].get(key.get((x["N"], x["K"]), ""), {}) for x in shapes]
     import re
-    m = re.fullmatch(r"dl_bn(\d+)_bm(\d+)_w(\d+)x(\d+)_s(\d+)(?:_k(\d+))?", cfg_name)
+    m = re.fullmatch(r"dl_bn(\d+)_bm(\d+)_w(\d+)x(\d+)_s(\d+)(?:_k(\d+))?(?:_u(\d+))?", cfg_name)
     if m:
         g = m.groups()
-        tag = "k_gemm_dl<{}, {}, {}, {}, {}, false, {}>".format(*g[:5], g[5] or 1)
+        tag = "k_gemm_dl<{}, {}, {}, {}, {}, false, {}, {}>".format(*g[:5], g[5] or 1, g[6] or 1)
     else:
         m = re.fullmatch(r"bn(\d+)_bm(\d+)_bk(\d+)_w(\d+)x(\d+)_d(\d+)", cfg_name)
         if not m:
