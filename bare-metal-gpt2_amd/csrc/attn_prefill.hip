@@ -55,7 +55,9 @@ __device__ __forceinline__ float group_sum(float v) {
 }
 
 __global__ __launch_bounds__(64 * AP_W) void k_attn_prefill_mfma(uint16_t *__restrict__ att,
-                                                                  const uint16_t *__restrict__ qkv, int T) {
+                                                                  const uint16_t *__restrict__ qkv, int T,
+                                                                  uint16_t *__restrict__ Kc, uint16_t *__restrict__ Vc,
+                                                                  int maxT) {
     constexpr int E = GPT2_N_EMBD, D = GPT2_HEAD_DIM, S3 = 3 * GPT2_N_EMBD;
     static_assert(D == 64 && AP_QB == 16 && AP_CK == 32, "fragment layout is written for these sizes");
     __shared__ __attribute__((aligned(16))) char vt_all[AP_W][D * AP_RS];
@@ -82,6 +84,15 @@ __global__ __launch_bounds__(64 * AP_W) void k_attn_prefill_mfma(uint16_t *__res
     }
     if (qi >= nb) return;                      // the grid is rounded up (whole work-group leaves)
     const int q0 = (nb - 1 - qi) * AP_QB;
+    if (Kc) {
+        // The prefill's K/V cache rows of this block's positions and head, one 16-byte chunk per
+        // thread (16 positions x 8 chunks for K, the same for V), into [H][maxT][D] of the layer.
+        static_assert(2 * AP_QB * (D / 8) == 64 * AP_W, "one chunk per thread");
+        const int t = q0 + ((threadIdx.x >> 3) & (AP_QB - 1)), d8 = (threadIdx.x & 7) * 8, v = threadIdx.x >> 7;
+        if (t < T)
+            *reinterpret_cast<f16x8 *>((v ? Vc : Kc) + ((size_t)h * maxT + t) * D + d8) =
+                *reinterpret_cast<const f16x8 *>(qkv + (size_t)t * S3 + (v ? 2 * E : E) + h * D + d8);
+    }
     const int qlast = min(q0 + AP_QB, T) - 1;
     const int nc = qlast / AP_CK + 1;          // chunks over keys [0, qlast]; chunk start <= q0
     const int q = q0 + jq;                     // this lane's query (q >= T: computed, not stored)
@@ -226,9 +237,12 @@ __global__ __launch_bounds__(64 * AP_W) void k_attn_prefill_mfma(uint16_t *__res
     }
 }
 
-void attention_prefill(uint16_t *att, const uint16_t *qkv, int T) {
+// Kc, Vc (optional): the layer's K and V cache planes ([H][maxT][D]), filled with this prompt's rows
+// (the prefill scatter of cuda/kvcache.cu:66-81, done inside the attention launch).
+void attention_prefill(uint16_t *att, const uint16_t *qkv, int T, uint16_t *Kc, uint16_t *Vc, int maxT) {
     static_assert(GPT2_N_HEAD == 12, "the XCD assignment covers 12 heads on 8 XCDs");
-    hipLaunchKernelGGL(k_attn_prefill_mfma, dim3(8 * 3 * cdiv(cdiv(T, AP_QB), 2)), dim3(64 * AP_W), 0, stream(), att, qkv, T);
+    hipLaunchKernelGGL(k_attn_prefill_mfma, dim3(8 * 3 * cdiv(cdiv(T, AP_QB), 2)), dim3(64 * AP_W), 0, stream(), att, qkv, T, Kc, Vc,
+                       maxT);
     check_launch("k_attn_prefill_mfma");
 }
 

@@ -99,9 +99,41 @@ __device__ __forceinline__ uint16_t f2h(float f) {
 }
 
 // gelu_new, the tanh form (model/config.h:41-42): 0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))).
+// The decode kernels (fused GEMV epilogue, persistent step) use this form.
 __device__ __forceinline__ float gelu_tanh(float v) {
     const float z = 0.7978845608028654f * (v + 0.044715f * v * v * v);
     return 0.5f * v * (1.0f + tanhf(z));
+}
+
+// gelu_new rounded to fp16 for the prefill, where the elementwise gelu kernel and the fused GEMM
+// epilogue must agree bit for bit.  With 1 + tanh(z) = 2 / (1 + e^(-2z)), gelu is v / (1 + e^(-2z)),
+// computed as v * rcp(1 + 2^(K * (v + 0.044715 v^3))), K = -2 sqrt(2/pi) log2(e), on the hardware
+// exp2 and reciprocal (a few fp32 ulps) with explicit builtins and one explicit fma, so nothing is
+// left to contract or reassociate.  The fp32 result is pinned before the conversion: otherwise the
+// conversion folds into the last multiply in some kernels (v_fma_mixlo_f16: one rounding) and not in
+// others (fp32 product, then convert: two roundings, 1 ulp apart on rare ties).  Large |v|: the
+// exponential goes to 0 or +inf and the result to v or -0.
+__device__ __forceinline__ uint16_t gelu_f16(float v) {
+    constexpr float K = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
+    const float inner = __builtin_fmaf(0.044715f, v * v * v, v);
+    const float e = __builtin_amdgcn_exp2f(K * inner);
+    float y = v * __builtin_amdgcn_rcpf(1.0f + e);
+    asm volatile("" : "+v"(y));
+    return f2h(y);
+}
+
+// Elementwise op fused into a matmul's epilogue: none, gelu_new, or a residual add.
+enum { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2 };
+
+// A GEMM output after scale and bias, as the unfused sequence would leave it: rounded to fp16, then
+// gelu (rounded again) or the residual r added (rounded again) -- the rounding points of a separate
+// matmul, gelu and add (cuda/forward_cuda.cu:99-105), so fusing changes no bit.
+template <int EPI>
+__device__ __forceinline__ uint16_t epi_out(float v, uint16_t r) {
+    uint16_t o = f2h(v);
+    if constexpr (EPI == EPI_GELU) o = gelu_f16(h2f(o));
+    else if constexpr (EPI == EPI_RESID) o = f2h(h2f(r) + h2f(o));
+    return o;
 }
 
 // Sign-exact int8 -> fp16 for four packed bytes: (b ^ 0x80) is b + 128 in [1, 255]; the half with

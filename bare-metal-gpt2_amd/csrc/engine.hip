@@ -15,6 +15,9 @@ namespace g2 {
 void gemv(uint16_t *C, const uint16_t *x, const void *W, const float *Ws, const uint16_t *bias, int N, int K, bool qw,
           int cfg);
 void embed_one(uint16_t *x, const uint16_t *wte, const uint16_t *wpe, StepArg st);
+bool gemm_fused(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const uint16_t *bias, int M, int N,
+                int K, bool qw, int epi, const uint16_t *resid);
+void attention_prefill(uint16_t *att, const uint16_t *qkv, int T, uint16_t *Kc, uint16_t *Vc, int maxT);
 void kv_append(uint16_t *K, uint16_t *V, const uint16_t *qkv, StepArg st, int maxT);
 void attn_decode(uint16_t *att, const uint16_t *qkv, const uint16_t *K, const uint16_t *V, int maxT, StepArg st,
                  int len_imm);
@@ -22,7 +25,6 @@ void argmax_advance(const uint16_t *logits, int V, int *state, int *tokens, int 
 void attn_decode_append(uint16_t *att, const uint16_t *qkv, uint16_t *K, uint16_t *V, int maxT, StepArg st);
 bool gemv_fused(uint16_t *C, const uint16_t *x, const void *W, const float *Ws, const uint16_t *bias, int N, int K,
                 bool qw, const uint16_t *ln_g, const uint16_t *ln_b, int epi, const uint16_t *resid);
-enum { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2 };
 }  // namespace g2
 
 using namespace g2;
@@ -202,6 +204,38 @@ extern "C" void gpt2_scratch_free(GPT2ScratchGPU *s) {
 // ============================================================================ prefill forward
 static void capcpy(gpt2_half *dst, const gpt2_half *src, size_t n) { gpt2_d2d(dst, src, n * 2); }
 
+// When the backend's matmul, gelu, add and attention slots are this library's, the prefill runs
+// fused: gelu in the fc GEMM's epilogue, the residual adds in the attn-proj and mlp-proj epilogues,
+// the K/V cache fill inside the attention launch -- 5 launches per layer instead of 9, each result
+// bit-identical to the unfused sequence (same fp16 rounding points).  Other backends, and shapes the
+// fused GEMM does not take, run the reference's sequence (cuda/forward_cuda.cu:90-106).
+static bool g_prefill_fused = true;   // gpt2_tune_prefill_fused (tests compare both sequences)
+static bool fused_prefill_ok(const GPT2Backend *be) {
+    return g_prefill_fused && be->matmul == gpt2_matmul_tiled &&
+           (be->matmul_q == nullptr || be->matmul_q == gpt2_matmul_int8) && be->gelu == gpt2_gelu && be->add == gpt2_add;
+}
+
+// Tuning/test hook (not part of the reference interface): 0 makes every prefill run the unfused
+// reference sequence, 1 (the default) restores the fused one.
+extern "C" void gpt2_tune_prefill_fused(int on) { g_prefill_fused = on != 0; }
+
+// One prefill matmul site followed by `epi` (gelu in place, or C = resid + product): fused when
+// allowed and the GEMM takes it, else the backend's matmul into `tmp` (EPI_RESID) or C, then gelu/add.
+static void matmul_site(const GPT2Backend *be, bool fused, gpt2_half *C, const gpt2_half *A, const gpt2_half *Wh,
+                        const GPT2QW *Wq, const gpt2_half *bias, int M, int N, int K, int epi, gpt2_half *tmp) {
+    const bool q = be->matmul_q && Wq && Wq->q;
+    if (fused && gemm_fused(C, A, q ? (const void *)Wq->q : (const void *)Wh, q ? Wq->s : nullptr, bias, M, N, K, q,
+                            epi, epi == EPI_RESID ? C : nullptr))
+        return;
+    if (epi == EPI_RESID) {
+        gpt2_matmul_dispatch(be, tmp, A, Wh, Wq, bias, M, N, K);
+        be->add(C, tmp, (size_t)M * N);
+    } else {
+        gpt2_matmul_dispatch(be, C, A, Wh, Wq, bias, M, N, K);
+        if (epi == EPI_GELU) be->gelu(C, (size_t)M * N);
+    }
+}
+
 extern "C" void gpt2_forward_cuda(const GPT2Backend *be, const GPT2WeightsGPU *w, const int *d_ids, int T,
                                   GPT2ScratchGPU *s, GPT2CapsGPU *caps) {
     if (!be || !w || !w->data || !s || !d_ids || T <= 0 || T > s->maxT || T > GPT2_N_CTX) {
@@ -213,6 +247,9 @@ extern "C" void gpt2_forward_cuda(const GPT2Backend *be, const GPT2WeightsGPU *w
     GPT2KVCache *kv = caps ? caps->kv : nullptr;
     if (kv && T > kv->maxT) { arg_fail("gpt2_forward_cuda: T exceeds the KV cache"); return; }
 
+    const bool fused = fused_prefill_ok(be);
+    // the attention launch fills the cache itself when it is this library's prefill attention
+    const bool attn_kv = fused && be->attention == gpt2_attention_flash && kv && kv->data;
     be->embed(s->x, w->wte, w->wpe, d_ids, T, E);
     if (caps && caps->embed) capcpy(caps->embed, s->x, (size_t)T * E);
     for (int L = 0; L < GPT2_N_LAYER; ++L) {
@@ -220,15 +257,18 @@ extern "C" void gpt2_forward_cuda(const GPT2Backend *be, const GPT2WeightsGPU *w
         const GPT2QLayerGPU *qy = qw ? &qw->layers[L] : nullptr;
         be->layernorm(s->ln, s->x, ly->ln1_g, ly->ln1_b, T, E);
         gpt2_matmul_dispatch(be, s->qkv, s->ln, ly->qkv_w, qy ? &qy->qkv_w : nullptr, ly->qkv_b, T, Q, E);
-        if (kv) gpt2_kv_scatter_prefill(kv, L, s->qkv, T);
-        be->attention(s->att, s->qkv, T, E, H, D);
-        gpt2_matmul_dispatch(be, s->ao, s->att, ly->attn_proj_w, qy ? &qy->attn_proj_w : nullptr, ly->attn_proj_b, T, E, E);
-        be->add(s->x, s->ao, (size_t)T * E);
+        if (attn_kv && L < kv->nLayer) {
+            attention_prefill(s->att, s->qkv, T, gpt2_kv_K(kv, L), gpt2_kv_V(kv, L), kv->maxT);
+        } else {
+            if (kv) gpt2_kv_scatter_prefill(kv, L, s->qkv, T);
+            be->attention(s->att, s->qkv, T, E, H, D);
+        }
+        matmul_site(be, fused, s->x, s->att, ly->attn_proj_w, qy ? &qy->attn_proj_w : nullptr, ly->attn_proj_b, T, E, E,
+                    EPI_RESID, s->ao);
         be->layernorm(s->ln, s->x, ly->ln2_g, ly->ln2_b, T, E);
-        gpt2_matmul_dispatch(be, s->fc, s->ln, ly->fc_w, qy ? &qy->fc_w : nullptr, ly->fc_b, T, F, E);
-        be->gelu(s->fc, (size_t)T * F);
-        gpt2_matmul_dispatch(be, s->ff, s->fc, ly->proj_w, qy ? &qy->proj_w : nullptr, ly->proj_b, T, E, F);
-        be->add(s->x, s->ff, (size_t)T * E);
+        matmul_site(be, fused, s->fc, s->ln, ly->fc_w, qy ? &qy->fc_w : nullptr, ly->fc_b, T, F, E, EPI_GELU, nullptr);
+        matmul_site(be, fused, s->x, s->fc, ly->proj_w, qy ? &qy->proj_w : nullptr, ly->proj_b, T, E, F, EPI_RESID,
+                    s->ff);
         if (caps && caps->blocks) capcpy(caps->blocks + (size_t)L * T * E, s->x, (size_t)T * E);
     }
     be->layernorm(s->ln, s->x, w->lnf_g, w->lnf_b, T, E);

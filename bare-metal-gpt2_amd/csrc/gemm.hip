@@ -62,7 +62,9 @@ template <int BN, int BM, int BK, int WN, int WM, bool QW, int DEPTH, bool GUARD
 __global__ __launch_bounds__(256) void k_gemm_mfma(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
                                                    const void *__restrict__ Wv, const float *__restrict__ Ws,
                                                    const uint16_t *__restrict__ bias, int M, int N, int K,
-                                                   int tiles_m, int ntiles, int vec_store) {
+                                                   int tiles_m, int ntiles, int vec_store,
+                                                   const uint16_t *resid) {
+    (void)resid;   // the fused epilogues live in k_gemm_dl
     static_assert(WN * WM == 4, "four waves per work-group");
     constexpr int CH = BK / 8;               // 16-byte chunks per LDS row
     constexpr int WTN = BN / WN, WTM = BM / WM;  // wave tile
@@ -291,11 +293,13 @@ __device__ __forceinline__ f16x8 i8x8_to_f16x8(uint2 w) {
 // groups 1.. add their accumulators into group 0's through LDS before the epilogue.
 // U > 1 covers U consecutive k-tiles per barrier: their fragments are read back to back (one LDS
 // round trip) and then multiplied, and U tiles are refilled at a time (S % U == 0, S >= 2U).
-template <int BN, int BM, int WN, int WM, int S, bool QW, int KS = 1, int U = 1>
+// EPI: the elementwise op fused into the epilogue (EPI_GELU; EPI_RESID adds resid, which may be C).
+template <int BN, int BM, int WN, int WM, int S, bool QW, int KS = 1, int U = 1, int EPI = EPI_NONE>
 __global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
                                                          const void *__restrict__ Wv, const float *__restrict__ Ws,
                                                          const uint16_t *__restrict__ bias, int M, int N, int K,
-                                                         int tiles_m, int ntiles, int vec_store) {
+                                                         int tiles_m, int ntiles, int vec_store,
+                                                         const uint16_t *resid) {
 #if defined(__HIP_DEVICE_COMPILE__)   // LDS address-space pointers exist only in the device pass
     constexpr int NW = WN * WM;
     constexpr int BK = 64;
@@ -491,12 +495,19 @@ __global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restri
 #pragma unroll
             for (int b = 0; b < TM; ++b) {
                 const int ml = wm0 + b * 16 + lrow;
+                uint16_t r[4] = {0, 0, 0, 0};
+                if (EPI == EPI_RESID && m0 + ml < M) {
+                    const uint16_t *rp = resid + (size_t)(m0 + ml) * N + nb;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (nb + i < N) r[i] = rp[i];
+                }
                 uint16_t o[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     float v = acc[a][b][i];
                     if constexpr (QW) v = v * sc[i];
-                    o[i] = f2h(v + bs[i]);
+                    o[i] = epi_out<EPI>(v + bs[i], r[i]);
                 }
                 *reinterpret_cast<uint2 *>(ct + ml * CS + nl) =
                     uint2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
@@ -531,12 +542,24 @@ __global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restri
         for (int b = 0; b < TM; ++b) {
             const int m = m0 + wm0 + b * 16 + lrow;
             if (m >= M) continue;
+            uint16_t r[4] = {0, 0, 0, 0};   // residual (EPI_RESID; may alias C: same lane reads, then writes)
+            if constexpr (EPI == EPI_RESID) {
+                const uint16_t *rp = resid + (size_t)m * N + nb;
+                if (vec_store && nb + 3 < N) {
+                    const uint2 rv = *reinterpret_cast<const uint2 *>(rp);
+                    r[0] = (uint16_t)rv.x; r[1] = (uint16_t)(rv.x >> 16); r[2] = (uint16_t)rv.y; r[3] = (uint16_t)(rv.y >> 16);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (nb + i < N) r[i] = rp[i];
+                }
+            }
             uint16_t o[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float v = acc[a][b][i];
                 if constexpr (QW) v = v * sc[i];
-                o[i] = f2h(v + bs[i]);
+                o[i] = epi_out<EPI>(v + bs[i], r[i]);
             }
             uint16_t *dst = C + (size_t)m * N + nb;
             if (vec_store && nb + 3 < N) {
@@ -595,38 +618,51 @@ __global__ void k_gemm_naive(uint16_t *__restrict__ C, const uint16_t *__restric
 }
 
 // ---------------------------------------------------------------------------- tile table
+typedef void (*GemmFn)(uint16_t *, const uint16_t *, const void *, const float *, const uint16_t *, int, int, int, int,
+                       int, int, const uint16_t *);
 struct GemmCfg {
-    int bn, bm, kmul;   // K must be a multiple of kmul (BK * DEPTH, or 8 for the guarded kernel)
-    int kmin, threads;  // and at least kmin; work-group size
-    void (*fp16)(uint16_t *, const uint16_t *, const void *, const float *, const uint16_t *, int, int, int, int, int, int);
-    void (*int8)(uint16_t *, const uint16_t *, const void *, const float *, const uint16_t *, int, int, int, int, int, int);
+    int bn, bm, kmul;    // K must be a multiple of kmul (BK * DEPTH, or 8 for the guarded kernel)
+    int kmin, threads;   // and at least kmin; work-group size
+    GemmFn fp16, int8;
+    GemmFn fused[2][2];  // [int8][gelu, residual]: fused-epilogue kernels, on the configs the prefill picks
+    bool dl;             // direct-to-LDS pipeline
     const char *name;
 };
 
+#define G2_NOFUSE {{nullptr, nullptr}, {nullptr, nullptr}}
+#define G2_FUSE(BN, BM, WN, WM, S, KS, U) \
+    {{k_gemm_dl<BN, BM, WN, WM, S, false, KS, U, EPI_GELU>, k_gemm_dl<BN, BM, WN, WM, S, false, KS, U, EPI_RESID>}, \
+     {k_gemm_dl<BN, BM, WN, WM, S, true, KS, U, EPI_GELU>, k_gemm_dl<BN, BM, WN, WM, S, true, KS, U, EPI_RESID>}}
 #define G2_CFG(BN, BM, BK, WN, WM, D) \
     {BN, BM, BK * D, 0, 256, k_gemm_mfma<BN, BM, BK, WN, WM, false, D>, k_gemm_mfma<BN, BM, BK, WN, WM, true, D>, \
-     "bn" #BN "_bm" #BM "_bk" #BK "_w" #WN "x" #WM "_d" #D}
-// Direct-to-LDS pipeline: K % 64 == 0 and at least S-1 k-tiles (per k group: K % (64 KS) == 0).
-#define G2_DCFG(BN, BM, WN, WM, S) \
+     G2_NOFUSE, false, "bn" #BN "_bm" #BM "_bk" #BK "_w" #WN "x" #WM "_d" #D}
+// Direct-to-LDS pipeline: K % 64 == 0 and at least S-1 k-tiles (per k group: K % (64 KS) == 0);
+// the ...F forms also carry the fused-epilogue kernels.
+#define G2_DCFG_(BN, BM, WN, WM, S, FUSE) \
     {BN, BM, 64, 64 * (S - 1), 64 * WN * WM, k_gemm_dl<BN, BM, WN, WM, S, false>, k_gemm_dl<BN, BM, WN, WM, S, true>, \
-     "dl_bn" #BN "_bm" #BM "_w" #WN "x" #WM "_s" #S}
+     FUSE, true, "dl_bn" #BN "_bm" #BM "_w" #WN "x" #WM "_s" #S}
+#define G2_DCFG(BN, BM, WN, WM, S) G2_DCFG_(BN, BM, WN, WM, S, G2_NOFUSE)
+#define G2_DCFGF(BN, BM, WN, WM, S) G2_DCFG_(BN, BM, WN, WM, S, G2_FUSE(BN, BM, WN, WM, S, 1, 1))
 #define G2_DCFGK(BN, BM, WN, WM, S, KS) \
     {BN, BM, 64 * KS, 64 * KS * (S - 1), 64 * WN * WM * KS, k_gemm_dl<BN, BM, WN, WM, S, false, KS>, \
-     k_gemm_dl<BN, BM, WN, WM, S, true, KS>, "dl_bn" #BN "_bm" #BM "_w" #WN "x" #WM "_s" #S "_k" #KS}
+     k_gemm_dl<BN, BM, WN, WM, S, true, KS>, G2_NOFUSE, true, "dl_bn" #BN "_bm" #BM "_w" #WN "x" #WM "_s" #S "_k" #KS}
 // ... and U k-tiles per barrier: K % (64 KS U) == 0, at least S-U k-tiles per group.
-#define G2_DCFGU(BN, BM, WN, WM, S, KS, U) \
+#define G2_DCFGU_(BN, BM, WN, WM, S, KS, U, FUSE) \
     {BN, BM, 64 * KS * U, 64 * KS * (S - U), 64 * WN * WM * KS, k_gemm_dl<BN, BM, WN, WM, S, false, KS, U>, \
-     k_gemm_dl<BN, BM, WN, WM, S, true, KS, U>, "dl_bn" #BN "_bm" #BM "_w" #WN "x" #WM "_s" #S "_k" #KS "_u" #U}
+     k_gemm_dl<BN, BM, WN, WM, S, true, KS, U>, FUSE, true, \
+     "dl_bn" #BN "_bm" #BM "_w" #WN "x" #WM "_s" #S "_k" #KS "_u" #U}
+#define G2_DCFGU(BN, BM, WN, WM, S, KS, U) G2_DCFGU_(BN, BM, WN, WM, S, KS, U, G2_NOFUSE)
+#define G2_DCFGUF(BN, BM, WN, WM, S, KS, U) G2_DCFGU_(BN, BM, WN, WM, S, KS, U, G2_FUSE(BN, BM, WN, WM, S, KS, U))
 static const GemmCfg kCfgs[] = {
-    G2_DCFG(96, 64, 2, 4, 4),       // 0: 8 waves, wave tile 48x16
+    G2_DCFGF(96, 64, 2, 4, 4),      // 0: 8 waves, wave tile 48x16
     G2_DCFG(128, 64, 4, 2, 3),      // 1: 8 waves, wave tile 32x32
-    G2_DCFG(32, 64, 1, 4, 4),       // 2: 4 waves, wave tile 32x16
-    G2_DCFG(64, 32, 2, 2, 4),       // 3: 4 waves, wave tile 32x16
+    G2_DCFGF(32, 64, 1, 4, 4),      // 2: 4 waves, wave tile 32x16
+    G2_DCFGF(64, 32, 2, 2, 4),      // 3: 4 waves, wave tile 32x16
     G2_DCFG(96, 64, 2, 2, 6),       // 4: 4 waves, wave tile 48x32
-    G2_DCFG(64, 64, 2, 4, 4),       // 5: 8 waves, wave tile 32x16
-    G2_DCFG(128, 128, 2, 4, 4),     // 6: 8 waves, wave tile 64x32
+    G2_DCFGF(64, 64, 2, 4, 4),      // 5: 8 waves, wave tile 32x16
+    G2_DCFGF(128, 128, 2, 4, 4),    // 6: 8 waves, wave tile 64x32
     G2_DCFG(256, 128, 4, 2, 3),     // 7: 8 waves, wave tile 64x64
-    G2_DCFG(32, 32, 1, 2, 4),       // 8: 2 waves, wave tile 32x16
+    G2_DCFGF(32, 32, 1, 2, 4),      // 8: 2 waves, wave tile 32x16
     G2_DCFG(48, 32, 3, 2, 4),       // 9: 6 waves, wave tile 16x16
     G2_DCFG(48, 32, 1, 2, 4),       // 10: 2 waves, wave tile 48x16
     G2_DCFG(48, 32, 3, 2, 6),       // 11: 6 waves, wave tile 16x16, 6 stages
@@ -641,17 +677,17 @@ static const GemmCfg kCfgs[] = {
     G2_DCFG(48, 64, 3, 4, 4),       // 20: 12 waves, wave tile 16x16
     G2_DCFGK(128, 64, 4, 2, 3, 2),  // 21: two k groups of 8 waves
     G2_DCFGU(48, 32, 3, 2, 4, 2, 2),  // 22: as 15, two k-tiles per barrier
-    G2_DCFGU(48, 32, 3, 2, 6, 2, 2),  // 23: as 15, two k-tiles per barrier, 6 stages (mlp-proj)
+    G2_DCFGUF(48, 32, 3, 2, 6, 2, 2), // 23: as 15, two k-tiles per barrier, 6 stages (mlp-proj)
     G2_DCFGU(48, 32, 3, 2, 4, 1, 2),  // 24: as 9, two k-tiles per barrier (QKV)
     G2_DCFGU(48, 32, 3, 2, 6, 1, 2),  // 25: as 9, two k-tiles per barrier, 6 stages
-    G2_DCFGU(48, 64, 3, 4, 4, 1, 2),  // 26: as 20, two k-tiles per barrier (fc)
+    G2_DCFGUF(48, 64, 3, 4, 4, 1, 2), // 26: as 20, two k-tiles per barrier (fc)
     G2_DCFGU(48, 64, 3, 4, 6, 1, 2),  // 27: as 20, two k-tiles per barrier, 6 stages
     G2_DCFGU(48, 32, 3, 2, 6, 1, 3),  // 28: as 9, three k-tiles per barrier
     G2_DCFGU(48, 64, 3, 4, 6, 1, 3),  // 29: as 20, three k-tiles per barrier
     G2_DCFGU(48, 32, 3, 2, 6, 2, 3),  // 30: as 15, three k-tiles per barrier
-    G2_DCFGU(48, 32, 3, 2, 8, 1, 4),  // 31: as 9, four k-tiles per barrier (attn-proj)
+    G2_DCFGUF(48, 32, 3, 2, 8, 1, 4), // 31: as 9, four k-tiles per barrier (attn-proj)
     G2_DCFGU(48, 64, 3, 4, 8, 1, 4),  // 32: as 20, four k-tiles per barrier
-    G2_DCFGU(48, 32, 3, 2, 8, 2, 4),  // 33: as 15, four k-tiles per barrier (160 KB of LDS; INT8 mlp-proj)
+    G2_DCFGUF(48, 32, 3, 2, 8, 2, 4), // 33: as 15, four k-tiles per barrier (160 KB of LDS; INT8 mlp-proj)
     // register-ring pipeline (k_gemm_mfma): reference points for tuning
     G2_CFG(96, 64, 64, 2, 2, 6),    // 34: wave tile 48x32
     G2_CFG(64, 32, 64, 2, 2, 6),    // 35: wave tile 32x16
@@ -664,7 +700,7 @@ static_assert(sizeof(kCfgs) / sizeof(kCfgs[0]) == 38, "the pick table names conf
 // Any K % 8 == 0 (int8: K % 16 == 0): predicated loads, one k-tile of prefetch.
 #define G2_GCFG(BN, BM, WN, WM) \
     {BN, BM, 8, 0, 256, k_gemm_mfma<BN, BM, 64, WN, WM, false, 1, true>, k_gemm_mfma<BN, BM, 64, WN, WM, true, 1, true>, \
-     "guard_bn" #BN "_bm" #BM}
+     G2_NOFUSE, false, "guard_bn" #BN "_bm" #BM}
 static const GemmCfg kGuardCfgs[] = {
     G2_GCFG(64, 64, 2, 2),
     G2_GCFG(64, 32, 2, 2),
@@ -726,13 +762,13 @@ static bool mfma_ok(const void *A, const void *W, int K, bool qw) {
     return (K % 8) == 0 && aligned16(A) && aligned16(W);
 }
 
-static void launch_gemm(const GemmCfg &g, uint16_t *C, const uint16_t *A, const void *W, const float *Ws,
-                        const uint16_t *bias, int M, int N, int K, bool qw) {
+static void launch_gemm(const GemmCfg &g, GemmFn fn, uint16_t *C, const uint16_t *A, const void *W, const float *Ws,
+                        const uint16_t *bias, int M, int N, int K, const uint16_t *resid = nullptr) {
     const int tiles_m = cdiv(M, g.bm), tiles_n = cdiv(N, g.bn);
     const int ntiles = tiles_m * tiles_n;
     const int vec = (N % 4 == 0) && (((uintptr_t)C & 7u) == 0);
-    auto fn = qw ? g.int8 : g.fp16;
-    hipLaunchKernelGGL(fn, dim3(ntiles), dim3(g.threads), 0, stream(), C, A, W, Ws, bias, M, N, K, tiles_m, ntiles, vec);
+    hipLaunchKernelGGL(fn, dim3(ntiles), dim3(g.threads), 0, stream(), C, A, W, Ws, bias, M, N, K, tiles_m, ntiles, vec,
+                       resid);
 }
 
 static bool gemm_args(const char *who, const void *C, const void *A, const void *W, int M, int N, int K) {
@@ -753,8 +789,8 @@ void gemm(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const 
     // K == 0 (an empty sum, C = bias or 0) falls through to the generic kernel.
     if (K > 0 && mfma_ok(A, W, K, qw)) {
         const int c = (cfg >= 0 && cfg < kNumCfgs && cfg_fits(cfg, K)) ? cfg : pick_cfg(M, N, K, qw);
-        if (c >= 0) launch_gemm(kCfgs[c], C, A, W, Ws, bias, M, N, K, qw);
-        else launch_gemm(kGuardCfgs[(long)cdiv(N, 64) * cdiv(M, 64) >= 256 ? 0 : 1], C, A, W, Ws, bias, M, N, K, qw);
+        const GemmCfg &g = c >= 0 ? kCfgs[c] : kGuardCfgs[(long)cdiv(N, 64) * cdiv(M, 64) >= 256 ? 0 : 1];
+        launch_gemm(g, qw ? g.int8 : g.fp16, C, A, W, Ws, bias, M, N, K);
         check_launch(qw ? "k_gemm_mfma<int8>" : "k_gemm_mfma<fp16>");
         return;
     }
@@ -762,6 +798,25 @@ void gemm(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const 
     if (qw) hipLaunchKernelGGL(k_gemm_generic<true>, grid, dim3(256), 0, stream(), C, A, W, Ws, bias, M, N, K);
     else hipLaunchKernelGGL(k_gemm_generic<false>, grid, dim3(256), 0, stream(), C, A, W, Ws, bias, M, N, K);
     check_launch("k_gemm_generic");
+}
+
+// C = A . W^T (+ bias) followed by the elementwise op `epi` (EPI_GELU, or EPI_RESID: C = resid +
+// product, resid may be C itself), in one launch.  Fused-epilogue kernels exist for the
+// direct-to-LDS configs the prefill picks; returns false (nothing launched) when the picked config
+// has none, for M = 1 (the GEMV), shapes or pointers the MFMA paths cannot take, or a resid that
+// does not share C's 8-byte alignment -- the caller then runs the unfused sequence.
+bool gemm_fused(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const uint16_t *bias, int M, int N,
+                int K, bool qw, int epi, const uint16_t *resid) {
+    if (M <= 1 || N <= 0 || K <= 0 || !mfma_ok(A, W, K, qw)) return false;
+    if (epi == EPI_RESID && (!resid || (((uintptr_t)resid ^ (uintptr_t)C) & 7u))) return false;
+    if (epi != EPI_GELU && epi != EPI_RESID) return false;
+    const int c = pick_cfg(M, N, K, qw);
+    if (c < 0) return false;
+    const GemmFn fn = kCfgs[c].fused[qw ? 1 : 0][epi == EPI_RESID ? 1 : 0];
+    if (!fn) return false;
+    launch_gemm(kCfgs[c], fn, C, A, W, Ws, bias, M, N, K, resid);
+    check_launch(qw ? "k_gemm_dl<int8> fused" : "k_gemm_dl<fp16> fused");
+    return true;
 }
 
 }  // namespace g2

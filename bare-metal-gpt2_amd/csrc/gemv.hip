@@ -56,7 +56,6 @@ __device__ __forceinline__ float slot_sum(float v) {
 }
 
 // Epilogues a decode step fuses into its GEMVs.
-enum { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2 };
 
 
 // LPR lanes per row, CPL 16-byte chunks per lane (row = LPR*CPL chunks), U rows per slot in flight.

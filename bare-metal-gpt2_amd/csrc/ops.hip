@@ -15,7 +15,8 @@
 #include "attn.h"
 
 namespace g2 {
-void attention_prefill(uint16_t *att, const uint16_t *qkv, int T);   // attn_prefill.hip
+void attention_prefill(uint16_t *att, const uint16_t *qkv, int T, uint16_t *Kc = nullptr, uint16_t *Vc = nullptr,
+                       int maxT = 0);   // attn_prefill.hip
 
 // ------------------------------------------------------------------ embed
 __global__ void k_embed(uint16_t *__restrict__ x, const uint16_t *__restrict__ wte, const uint16_t *__restrict__ wpe,
@@ -95,15 +96,10 @@ __global__ __launch_bounds__(256) void k_layernorm(uint16_t *__restrict__ out, c
 }
 
 // ------------------------------------------------------------------ gelu / add
-__device__ __forceinline__ float gelu_new(float v) {
-    const float z = 0.7978845608028654f * (v + 0.044715f * v * v * v);
-    return 0.5f * v * (1.0f + tanhf(z));
-}
-
 __global__ void k_gelu(uint16_t *__restrict__ x, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    x[i] = f2h(gelu_new(h2f(x[i])));
+    x[i] = gelu_f16(h2f(x[i]));
 }
 
 __global__ void k_gelu8(f16x8 *__restrict__ x, size_t n8) {
@@ -111,7 +107,7 @@ __global__ void k_gelu8(f16x8 *__restrict__ x, size_t n8) {
     if (i >= n8) return;
     f16x8 v = x[i];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) v[c] = (f16)gelu_new((float)v[c]);
+    for (int c = 0; c < 8; ++c) v[c] = __builtin_bit_cast(f16, gelu_f16((float)v[c]));
     x[i] = v;
 }
 

@@ -117,6 +117,50 @@ def test_prefill_forward_backends_agree(pkg, L, synth, model):
         assert rel_err(outs[be], outs["flash"]) <= 5e-3, be
 
 
+@pytest.mark.parametrize("backend,T", [("flash", 200), ("int8", 200), ("tiled", 33), ("int8", 512)])
+def test_fused_prefill_bit_identical(pkg, L, synth, model, backend, T):
+    """The fused prefill (gelu and the residual adds in GEMM epilogues, the K/V cache fill inside the
+    attention launch) equals the unfused reference sequence bit for bit: every layer's residual
+    stream, the final LayerNorm, all logits rows and the whole K/V cache."""
+    ids = synth.token_ids(T, seed=T + 7)
+    d_ids = pkg.Dev.from_numpy(np.asarray(ids, np.int32))
+    if backend == "int8":
+        model.quantize()
+    runs = []
+    try:
+        for fused in (1, 0):
+            L.gpt2_tune_prefill_fused(fused)
+            scr, kv = pkg.Scratch(T), pkg.KVCache(T)
+            logits, blocks, fin = pkg.Dev(T * V * 2), pkg.Dev(12 * T * E * 2), pkg.Dev(T * E * 2)
+            caps = pkg.GPT2CapsGPU()
+            caps.logits, caps.logits_all, caps.final_ln, caps.blocks = logits.ptr, 1, fin.ptr, blocks.ptr
+            L.gpt2_memset(kv.kv.data, 0, kv.kv.bytes)
+            L.gpt2_prefill_fill_cache(pkg.backend(backend), C.byref(model.gpu), C.byref(kv.kv), d_ids.ptr, T,
+                                      C.byref(scr.s), C.byref(caps))
+            L.gpt2_sync()
+            pkg.check("prefill fused=%d" % fused)
+            assert kv.kv.len == T
+            cache = np.empty(kv.kv.bytes // 2, np.uint16)
+            assert L.gpt2_d2h(cache.ctypes.data, kv.kv.data, cache.nbytes) == 0
+            runs.append((blocks.numpy(np.uint16, (12 * T * E,)), fin.numpy(np.uint16, (T * E,)),
+                         logits.numpy(np.uint16, (T * V,)), cache))
+            scr.free()
+            kv.free()
+    finally:
+        L.gpt2_tune_prefill_fused(1)
+        if backend == "int8":
+            L.gpt2_quant_free(C.byref(model.q))
+            model.q = None
+            model.gpu.q = None
+    for name, a, b in zip(("blocks", "final_ln", "logits", "kv"), runs[0], runs[1]):
+        bad = np.flatnonzero(a != b)
+        where = ""
+        if bad.size and name == "blocks":
+            lyr, rem = np.divmod(bad[0], T * E)
+            where = f"first at layer {lyr}, row {rem // E}, column {rem % E}"
+        assert bad.size == 0, f"{name}: {bad.size} elements differ; {where}"
+
+
 def test_prefill_forward_int8(pkg, L, synth, body, model, deq_body):
     ids = synth.token_ids(20, seed=3)
     model.quantize()
