@@ -655,7 +655,7 @@ struct GemmCfg {
 #define G2_DCFGUF(BN, BM, WN, WM, S, KS, U) G2_DCFGU_(BN, BM, WN, WM, S, KS, U, G2_FUSE(BN, BM, WN, WM, S, KS, U))
 static const GemmCfg kCfgs[] = {
     G2_DCFGF(96, 64, 2, 4, 4),      // 0: 8 waves, wave tile 48x16
-    G2_DCFG(128, 64, 4, 2, 3),      // 1: 8 waves, wave tile 32x32
+    G2_DCFG(128, 64, 4, 2, 3),      // 1: 8 waves, wave tile 32x32 (vocabulary-sized N)
     G2_DCFGF(32, 64, 1, 4, 4),      // 2: 4 waves, wave tile 32x16
     G2_DCFGF(64, 32, 2, 2, 4),      // 3: 4 waves, wave tile 32x16
     G2_DCFG(96, 64, 2, 2, 6),       // 4: 4 waves, wave tile 48x32
@@ -746,6 +746,9 @@ static int pick_cfg(int M, int N, int K, bool qw = false) {
         else if (N == 3072 && K == 768) c = 26;           // fc: 48x64, 12 waves, 2 k-tiles/barrier
         if (c >= 0 && cfg_fits(c, K)) return c;
     }
+    // Vocabulary-sized N (the tied head, 50257 rows of W): many tiles per CU, bound by L2 bytes per
+    // FLOP, where large tiles win (M=512: 128x64 83 us, 256x128 88, 128x128 94, 48-row tiles >= 135).
+    if (N >= 16384 && M > 32 && cfg_fits(1, K)) return 1;
     const int order[] = {6, 0, 5, 2, 3, 8};
     int last = -1;
     for (int c : order) {

@@ -51,11 +51,15 @@ __global__ __launch_bounds__(256) void k_layernorm(uint16_t *__restrict__ out, c
     const uint16_t *xr = x + (size_t)row * E;
     uint16_t *o = out + (size_t)row * E;
     if constexpr (VEC768) {
-        // 768 = 3 x (64 lanes x 4 halves): keep the row in registers between the passes
+        // 768 = 3 x (64 lanes x 4 halves): keep the row in registers between the passes; gamma and
+        // beta are loaded with the row, so their latency hides behind the two reductions
         float v[12];
+        f16x4 gg[3], bb[3];
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
             const f16x4 h = *reinterpret_cast<const f16x4 *>(xr + 256 * i + 4 * lane);
+            gg[i] = *reinterpret_cast<const f16x4 *>(g + 256 * i + 4 * lane);
+            bb[i] = *reinterpret_cast<const f16x4 *>(b + 256 * i + 4 * lane);
 #pragma unroll
             for (int c = 0; c < 4; ++c) v[4 * i + c] = (float)h[c];
         }
@@ -73,11 +77,9 @@ __global__ __launch_bounds__(256) void k_layernorm(uint16_t *__restrict__ out, c
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
             const int e0 = 256 * i + 4 * lane;
-            const f16x4 gg = *reinterpret_cast<const f16x4 *>(g + e0);
-            const f16x4 bb = *reinterpret_cast<const f16x4 *>(b + e0);
             f16x4 r;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) r[c] = (f16)((v[4 * i + c] - mean) * rstd * (float)gg[c] + (float)bb[c]);
+            for (int c = 0; c < 4; ++c) r[c] = (f16)((v[4 * i + c] - mean) * rstd * (float)gg[i][c] + (float)bb[i][c]);
             *reinterpret_cast<f16x4 *>(o + e0) = r;
         }
         return;
@@ -333,7 +335,7 @@ extern "C" void gpt2_layernorm(gpt2_half *out, const gpt2_half *x, const gpt2_ha
     if (M <= 0 || E <= 0) return;
     if (!out || !x || !g || !b) { arg_fail("gpt2_layernorm: null pointer"); return; }
     if (E == GPT2_N_EMBD && !(((uintptr_t)x | (uintptr_t)out | (uintptr_t)g | (uintptr_t)b) & 7u))
-        hipLaunchKernelGGL(k_layernorm<true>, dim3(cdiv(M, 4)), dim3(256), 0, stream(), out, x, g, b, M, E);
+        hipLaunchKernelGGL(k_layernorm<true>, dim3(cdiv(M, 2)), dim3(128), 0, stream(), out, x, g, b, M, E);   // 2 rows per block
     else
         hipLaunchKernelGGL(k_layernorm<false>, dim3(cdiv(M, 4)), dim3(256), 0, stream(), out, x, g, b, M, E);
     check_launch("k_layernorm");
