@@ -688,14 +688,21 @@ static const GemmCfg kCfgs[] = {
     G2_DCFGUF(48, 32, 3, 2, 8, 1, 4), // 31: as 9, four k-tiles per barrier (attn-proj)
     G2_DCFGU(48, 64, 3, 4, 8, 1, 4),  // 32: as 20, four k-tiles per barrier
     G2_DCFGUF(48, 32, 3, 2, 8, 2, 4), // 33: as 15, four k-tiles per barrier (160 KB of LDS; INT8 mlp-proj)
+    G2_DCFGUF(48, 64, 3, 2, 4, 1, 2),   // 34: 6 waves, wave tile 16x32 (each widened INT8 fragment feeds 2 MFMAs)
+    G2_DCFGUF(48, 32, 3, 1, 4, 1, 2),   // 35: 3 waves, wave tile 16x32 (INT8 QKV, fc)
+    G2_DCFGU(48, 64, 3, 2, 4, 2, 2),    // 36: two k groups of 6 waves, wave tile 16x32
+    G2_DCFGU(96, 64, 3, 2, 4, 1, 2),    // 37: 6 waves, wave tile 32x32
+    G2_DCFGUF(48, 32, 3, 1, 8, 2, 4),   // 38: two k groups of 3 waves, 8 stages, 4 k-tiles per barrier
+    G2_DCFGUF(48, 32, 3, 1, 6, 2, 2),   // 39: two k groups of 3 waves, 6 stages
+    G2_DCFGUF(48, 32, 3, 1, 8, 1, 4),   // 40: 3 waves, 8 stages, 4 k-tiles per barrier
     // register-ring pipeline (k_gemm_mfma): reference points for tuning
-    G2_CFG(96, 64, 64, 2, 2, 6),    // 34: wave tile 48x32
-    G2_CFG(64, 32, 64, 2, 2, 6),    // 35: wave tile 32x16
-    G2_CFG(32, 64, 64, 1, 4, 6),    // 36: wave tile 32x16
-    G2_CFG(128, 128, 64, 2, 2, 2),  // 37: wave tile 64x64
+    G2_CFG(96, 64, 64, 2, 2, 6),    // 41: wave tile 48x32
+    G2_CFG(64, 32, 64, 2, 2, 6),    // 42: wave tile 32x16
+    G2_CFG(32, 64, 64, 1, 4, 6),    // 43: wave tile 32x16
+    G2_CFG(128, 128, 64, 2, 2, 2),  // 44: wave tile 64x64
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
-static_assert(sizeof(kCfgs) / sizeof(kCfgs[0]) == 38, "the pick table names configs by index");
+static_assert(sizeof(kCfgs) / sizeof(kCfgs[0]) == 45, "the pick table names configs by index");
 
 // Any K % 8 == 0 (int8: K % 16 == 0): predicated loads, one k-tile of prefetch.
 #define G2_GCFG(BN, BM, WN, WM) \
@@ -729,12 +736,14 @@ static int pick_cfg(int M, int N, int K, bool qw = false) {
     // gives about one work-group per CU (256 CUs), among the configs whose K constraint holds; -1
     // when none does (the guarded kernel runs).
     if (M > 256 && M <= 512 && qw) {
-        // INT8 weights (widened to fp16 as fragments are read), picked the same way: 421.5 us per
-        // 12-layer step against 467.3 with the fp16 picks of the previous table.
+        // INT8 weights (widened to fp16 as fragments are read), picked the same way on an INT8 step:
+        // QKV and fc take 16x32 wave tiles (3 waves), so each widened W fragment feeds two MFMAs and
+        // fewer waves widen the same rows (400.5 us per step, against 425.4 with the fp16 picks'
+        // shapes and 467.3 with the fp16 table itself).
         int c = -1;
-        if (N == 2304 && K == 768) c = 24;                // QKV: 48x32, 6 waves, 2 k-tiles/barrier
+        if (N == 2304 && K == 768) c = 35;                // QKV: 48x32, 3 waves, 2 k-tiles/barrier
         else if (N == 768 && K == 768) c = 31;            // attn-proj: 48x32, 8 stages, 4/barrier
-        else if (N == 3072 && K == 768) c = 26;           // fc: 48x64, 12 waves, 2/barrier
+        else if (N == 3072 && K == 768) c = 35;           // fc: as QKV
         else if (N == 768 && K == 3072) c = 33;           // mlp-proj: 48x32, 2 k groups, 8 stages, 4/barrier
         if (c >= 0 && cfg_fits(c, K)) return c;
     }
