@@ -21,6 +21,8 @@ Also reported in the same JSON line:
                 the 511-step greedy run
   cpu_baseline  the reference's own cpu/forward_cpu.c matmul (oracle/_ref, if built) or the oracle
                 restatement, on the same four GEMM shapes, on this host's cores
+  cpu_decode_baseline  the reference's CPU decode @ctx=512 (no KV cache: a full forward over 513
+                positions per token), tok/s beside the GPU decode leg
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras]
 """
@@ -430,6 +432,34 @@ def cpu_baseline(budget_s=12.0):
                       f" per set), fp32 storage / double accumulation, {dt:.1f} s"}
 
 
+def cpu_decode_baseline(budget_s=8.0):
+    """Decode tok/s @ctx=512 of the reference's CPU path (cpu/forward_cpu.c): it has no KV cache, so a
+    token is a full forward over 513 positions with last-row logits (bench/correctness.c:252-263,
+    92 GFLOP), on the same seeded body as the decode leg, fp32.  At least one token, more while the
+    budget lasts."""
+    import importlib
+    import oracle
+    threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
+    synth = importlib.import_module("bare_metal_gpt2_amd.synth")
+    body = synth.make_body(seed=1234, plain=True)
+    ids = synth.token_ids(513, seed=1234)
+    use_ref = oracle.ref_available()
+    off = oracle.oracle_offsets() if use_ref else None
+    n, t0 = 0, time.perf_counter()
+    while True:
+        if use_ref:
+            oracle.ref_forward(body, off, ids, logits_all=False)
+        else:
+            oracle.forward(body, ids, logits_all=False)
+        n += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 4), "unit": "tok/s", "cores": threads, "kind": "reference" if use_ref else "port",
+            "sample": f"{n} token(s) at ctx=512, each a full fp32 forward over 513 positions (no KV cache on the "
+                      f"reference CPU path), {dt:.1f} s"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -497,6 +527,9 @@ def main():
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
         log(f"cpu: {out['cpu_baseline']}")
+        if not args.no_extras and not args.no_decode:
+            out["cpu_decode_baseline"] = cpu_decode_baseline()
+            log(f"cpu decode: {out['cpu_decode_baseline']}")
     print(json.dumps(out), flush=True)
 
 
