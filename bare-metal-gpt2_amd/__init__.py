@@ -167,6 +167,7 @@ SIGNATURES = {
     "gpt2_decode_graph_time": (_i, [_vp, _i, _fp]),
     # bench / tuning hooks (not part of the reference interface)
     "gpt2_bench_ops": (_i, [C.POINTER(GPT2BenchOp), _i, _i, _i, _fp, _fp]),
+    "gpt2_bench_ops_graph": (_i, [C.POINTER(GPT2BenchOp), _i, _i, _i, _fp]),
     "gpt2_bench_time": (_i, [_vp, _vp, _fp]),
     "gpt2_device_info": (_i, [C.POINTER(_i), C.POINTER(_i), C.c_char_p, _i]),
     "gpt2_bench_empty": (_i, [_i, _fp]),

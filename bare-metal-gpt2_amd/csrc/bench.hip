@@ -67,6 +67,48 @@ int gpt2_bench_ops(const GPT2BenchOp *ops, int n, int warmup, int iters, float *
     return gpt2_last_error();
 }
 
+// The same timed rounds as gpt2_bench_ops, but one round of ops[0..n) is captured once into a
+// hipGraph on a stream of its own and each round is one replay of it (the launch cost of a prefill
+// captured per token count, as a server does for fixed prefill buckets).
+int gpt2_bench_ops_graph(const GPT2BenchOp *ops, int n, int warmup, int iters, float *ms_round) {
+    if (!ops || n <= 0 || iters <= 0) return 1;
+    hipStream_t prev = (hipStream_t)gpt2_get_stream(), s = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    hipEvent_t a = nullptr, b = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e == hipSuccess) {
+        gpt2_set_stream(s);
+        for (int i = 0; i < n; ++i) run_op(ops[i]);   // first launches outside the capture
+        e = hipStreamSynchronize(s);
+    }
+    if (e == hipSuccess) e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    if (e == hipSuccess) {
+        for (int i = 0; i < n; ++i) run_op(ops[i]);
+        e = hipStreamEndCapture(s, &graph);
+    }
+    gpt2_set_stream(prev);
+    if (e == hipSuccess) e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (e == hipSuccess) e = hipEventCreate(&a);
+    if (e == hipSuccess) e = hipEventCreate(&b);
+    for (int w = 0; e == hipSuccess && w < warmup; ++w) e = hipGraphLaunch(exec, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e == hipSuccess) e = hipEventRecord(a, s);
+    for (int it = 0; e == hipSuccess && it < iters; ++it) e = hipGraphLaunch(exec, s);
+    if (e == hipSuccess) e = hipEventRecord(b, s);
+    if (e == hipSuccess) e = hipEventSynchronize(b);
+    float ms = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+    if (e == hipSuccess && ms_round) *ms_round = ms / iters;
+    if (a) hipEventDestroy(a);
+    if (b) hipEventDestroy(b);
+    if (exec) hipGraphExecDestroy(exec);
+    if (graph) hipGraphDestroy(graph);
+    if (s) hipStreamDestroy(s);
+    if (e != hipSuccess) return (int)e;
+    return gpt2_last_error();
+}
+
 // Times `steps` graph replays (one decode token each) with events on the graph's stream.
 struct GPT2DecodeGraph;
 int gpt2_decode_graph_run(GPT2DecodeGraph *g, int steps);
