@@ -8,6 +8,8 @@ resident in HBM before the timed region; timing is hipEvents on the launch strea
 
 Also reported in the same JSON line:
   roofline      the GEMM kernel with the largest share of the step, against 2500 TFLOP/s fp16 MFMA
+  gemm_set_graph_replay  the same step captured once as a hipGraph and replayed (no faster: the
+                gap between dependent launches is the same inside a graph)
   gemv_int8     INT8 decode GEMV GB/s per trunk shape, cold (rotating > 512 MB of weight copies,
                 so every launch streams from HBM) and warm (same weights every launch), the
                 48-GEMV trunk chain of one decode step, and the same kernel on the INT8 tied head
@@ -16,11 +18,14 @@ Also reported in the same JSON line:
   gemm_int8_set the same P=512 trunk set with INT8 weights (the config-5 prefill GEMMs)
   head_gemm     the tied head as a prefill GEMM, [512x768] . [768x50257]^T (39.5 GFLOP)
   attention_prefill  causal MFMA prefill attention per launch at T=512 and T=1024 (12 heads x 64)
+  forward_t64   config 1 on the GPU: the fp16 forward at T=64 with logits for all 64 rows
   decode        GPT-2-124M decode tok/s @ctx=512: INT8 trunk + fp16 head, one hipGraph replay per
                 token, after a P=512 prefill (the prefill itself is timed too); plus the mean over
                 the 511-step greedy run
   cpu_baseline  the reference's own cpu/forward_cpu.c matmul (oracle/_ref, if built) or the oracle
                 restatement, on the same four GEMM shapes, on this host's cores
+  cpu_forward_t64  config 1 on the CPU: the reference's forward at T=64 with logits_all (median of
+                5 on every thread, one run on one thread), beside forward_t64
   cpu_decode_baseline  the reference's CPU decode @ctx=512 (no KV cache: a full forward over 513
                 positions per token), tok/s beside the GPU decode leg
 
@@ -30,6 +35,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes as C
+import importlib
 import json
 import os
 import sys
@@ -83,6 +89,16 @@ class Bench:
             raise RuntimeError(f"gpt2_bench_ops rc={rc}")
         return ms.value, (list(per) if per_op else None)
 
+    def run_ops_graph(self, ops, warmup, iters):
+        """Mean ms per round when one round is captured once as a hipGraph and replayed."""
+        arr = (self.pkg.GPT2BenchOp * len(ops))(*ops)
+        ms = C.c_float()
+        rc = self.L.gpt2_bench_ops_graph(arr, len(ops), warmup, iters, C.byref(ms))
+        if rc:
+            self.pkg.check("gpt2_bench_ops_graph")
+            raise RuntimeError(f"gpt2_bench_ops_graph rc={rc}")
+        return ms.value
+
 
 def f16(rng, shape, std):
     return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float16)
@@ -104,6 +120,7 @@ def bench_gemm_set(B, steps, warmup):
             ops.append(B.op(0, outs[name].ptr, A.ptr, W.ptr, None, b.ptr, M_PREFILL, N, K))
     flops_step = sum(2.0 * M_PREFILL * N * K for _, N, K in GEMM_SET) * N_LAYER
     ms_step, _ = B.run_ops(ops, warmup, steps)
+    ms_graph = B.run_ops_graph(ops, warmup, steps)
     # Per-kernel launch durations for the roofline, under the step's own conditions: each shape's
     # 12 layer GEMMs (distinct weights, so the weights are not L2-resident) back to back.
     shapes = []
@@ -128,7 +145,7 @@ def bench_gemm_set(B, steps, warmup):
                 "kernel": dom[0], "avg_launch_us": round(d["ms"] / d["launches"] * 1e3, 3),
                 "flops_per_launch": d["flops"] / d["launches"]}
     roofline.update(measured_traffic(dom[0], [x for x in shapes if x["kernel"] == dom[0]]))
-    return flops_step, ms_step, shapes, roofline
+    return flops_step, ms_step, shapes, roofline, ms_graph
 
 
 def measured_traffic(cfg_name, shapes):
@@ -306,15 +323,99 @@ def bench_attention(B):
     return res
 
 
+# ------------------------------------------------------------------------------ seeded body
+_BODY = None
+
+
+def seeded_body():
+    """The seeded GPT-2-124M body (base seed 1234, N(0,0.02) weights, zero biases, LN 1/0), built once
+    and shared by the forward, decode and CPU legs."""
+    global _BODY
+    if _BODY is None:
+        _BODY = importlib.import_module("bare_metal_gpt2_amd.synth").make_body(seed=1234, plain=True)
+    return _BODY
+
+
+# ------------------------------------------------------------------------------ forward (config 1)
+def bench_forward_t64(B, reps=20):
+    """Config 1 on the GPU: the fp16 forward (flash backend, fp16 weights) at T=64 with logits for
+    every row [64 x 50257] (forward_cuda.cu:77-116 with logits_all), host-timed per call around a
+    device sync; median, min and max of `reps` calls after 3 untimed ones."""
+    pkg, L = B.pkg, B.L
+    synth = importlib.import_module("bare_metal_gpt2_amd.synth")
+    model = pkg.Model(seeded_body())
+    T = 64
+    d_ids = B.dev(synth.token_ids(T, seed=1234))
+    logits = B.empty(T * VOCAB * 2)
+    scr = pkg.Scratch(T)
+    caps = pkg.GPT2CapsGPU()
+    caps.logits, caps.logits_all = logits.ptr, 1
+    be = pkg.backend("flash")
+    ms = []
+    for i in range(reps + 3):
+        L.gpt2_sync()
+        t = time.perf_counter()
+        L.gpt2_forward_cuda(be, C.byref(model.gpu), d_ids.ptr, T, C.byref(scr.s), C.byref(caps))
+        L.gpt2_sync()
+        if i >= 3:
+            ms.append((time.perf_counter() - t) * 1e3)
+    pkg.check("forward T=64")
+    model.free()
+    scr.free()
+    return {"T": T, "logits_all": True, "backend": "flash (fp16)", "gflop": 15.89,
+            "ms_median": round(float(np.median(ms)), 4), "ms_min_max": [round(min(ms), 4), round(max(ms), 4)]}
+
+
+def cpu_forward_t64():
+    """Config 1 on the CPU: the reference's forward (cpu/forward_cpu.c:118-166 via oracle/_ref, or the
+    restatement) at T=64 with logits_all, on the same seeded body and ids as bench_forward_t64.  Warmup
+    1, median of 5 on every thread, then one run on one thread (correctness.c:240-250 pattern)."""
+    import oracle
+    synth = importlib.import_module("bare_metal_gpt2_amd.synth")
+    body, ids = seeded_body(), synth.token_ids(64, seed=1234)
+    use_ref = oracle.ref_available()
+    off = oracle.oracle_offsets() if use_ref else None
+
+    def run():
+        t = time.perf_counter()
+        if use_ref:
+            oracle.ref_forward(body, off, ids, logits_all=True)
+        else:
+            oracle.forward(body, ids, logits_all=True)
+        return (time.perf_counter() - t) * 1e3
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
+    run()
+    ms = [run() for _ in range(5)]
+    one = None
+    try:
+        gomp = C.CDLL("libgomp.so.1")
+        gomp.omp_set_num_threads(1)
+        one = round(run(), 1)
+        gomp.omp_set_num_threads(threads)
+    except OSError:
+        pass
+    return {"T": 64, "logits_all": True, "kind": "reference" if use_ref else "port", "cores": threads,
+            "ms_median": round(float(np.median(ms)), 1), "ms_min_max": [round(min(ms), 1), round(max(ms), 1)],
+            "ms_one_thread": one, "gflop": 15.89, "cpu": cpu_model()}
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 # ------------------------------------------------------------------------------ decode (config 5)
 def bench_decode(B, steady_reps=64):
-    import importlib
     pkg, L = B.pkg, B.L
     synth = importlib.import_module("bare_metal_gpt2_amd.synth")
     t0 = time.time()
-    body = synth.make_body(seed=1234, plain=True)
-    model = pkg.Model(body)
-    del body
+    model = pkg.Model(seeded_body())
     model.quantize()                       # 48 trunk tensors INT8, head fp16
     kv = pkg.KVCache(1024)
     scr = pkg.Scratch(1024)
@@ -437,11 +538,10 @@ def cpu_decode_baseline(budget_s=8.0):
     token is a full forward over 513 positions with last-row logits (bench/correctness.c:252-263,
     92 GFLOP), on the same seeded body as the decode leg, fp32.  At least one token, more while the
     budget lasts."""
-    import importlib
     import oracle
     threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
     synth = importlib.import_module("bare_metal_gpt2_amd.synth")
-    body = synth.make_body(seed=1234, plain=True)
+    body = seeded_body()
     ids = synth.token_ids(513, seed=1234)
     use_ref = oracle.ref_available()
     off = oracle.oracle_offsets() if use_ref else None
@@ -496,7 +596,7 @@ def main():
         log(f"copy probe: {args.copy_probe} B in {ms.value * 1e3:.1f} us")
         src.free()
         dst.free()
-    flops_step, ms_step, shapes, roofline = bench_gemm_set(B, args.steps, args.warmup)
+    flops_step, ms_step, shapes, roofline, ms_graph = bench_gemm_set(B, args.steps, args.warmup)
     value = flops_step / (ms_step * 1e-3) / 1e12
     log(f"prefill GEMM set: {ms_step * 1e3:.1f} us/step -> {value:.1f} TFLOP/s; per shape {shapes}")
     out = {"metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -507,7 +607,9 @@ def main():
                                   "fp16 out (BASELINE config 2, per layer)",
                       "M": M_PREFILL, "layers": N_LAYER, "gflop_per_step": round(flops_step / 1e9, 4),
                       "device": name.value.decode()},
-           "roofline": roofline, "gemm_shapes": shapes}
+           "roofline": roofline, "gemm_shapes": shapes,
+           "gemm_set_graph_replay": {"us_per_step": round(ms_graph * 1e3, 2),
+                                     "tflops": round(flops_step / (ms_graph * 1e-3) / 1e12, 2)}}
     B.keep.clear()
     if not args.no_extras:
         gemv, head = bench_gemv(B)
@@ -520,6 +622,9 @@ def main():
         out["attention_prefill"] = bench_attention(B)
         B.keep.clear()
         log(f"attention: {out['attention_prefill']}")
+        out["forward_t64"] = bench_forward_t64(B)
+        B.keep.clear()
+        log(f"forward T=64: {out['forward_t64']}")
         if not args.no_decode:
             out["decode"] = bench_decode(B)
             B.keep.clear()
@@ -527,6 +632,9 @@ def main():
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
         log(f"cpu: {out['cpu_baseline']}")
+        if not args.no_extras:
+            out["cpu_forward_t64"] = cpu_forward_t64()
+            log(f"cpu forward T=64: {out['cpu_forward_t64']}")
         if not args.no_extras and not args.no_decode:
             out["cpu_decode_baseline"] = cpu_decode_baseline()
             log(f"cpu decode: {out['cpu_decode_baseline']}")
