@@ -573,7 +573,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the matmul path "
-              "would shard by output rows (see DESIGN.md), but no multi-GPU run is part of it.", file=sys.stderr)
+              "would shard by output rows (each GPU a slice of N), but no multi-GPU run is part of it.", file=sys.stderr)
         sys.exit(2)
     cpu_threads = max(1, min(16, os.cpu_count() or 1))
     os.environ.setdefault("OMP_NUM_THREADS", str(cpu_threads))
