@@ -164,7 +164,7 @@ def measured_traffic(cfg_name, shapes):
     m = re.fullmatch(r"dl_bn(\d+)_bm(\d+)_w(\d+)x(\d+)_s(\d+)(?:_k(\d+))?(?:_u(\d+))?", cfg_name)
     if m:
         g = m.groups()
-        tag = "k_gemm_dl<{}, {}, {}, {}, {}, false, {}, {}>".format(*g[:5], g[5] or 1, g[6] or 1)
+        tag = "k_gemm_dl<{}, {}, {}, {}, {}, false, {}, {}, 0>".format(*g[:5], g[5] or 1, g[6] or 1)
     else:
         m = re.fullmatch(r"bn(\d+)_bm(\d+)_bk(\d+)_w(\d+)x(\d+)_d(\d+)", cfg_name)
         if not m:
