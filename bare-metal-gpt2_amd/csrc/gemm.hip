@@ -418,6 +418,36 @@ __global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restri
             }
     };
 
+    // Epilogue operands (per-channel scales, bias, residual) are loaded here, ahead of the first
+    // k-tiles: they land long before the last MFMA instead of costing the epilogue a memory round
+    // trip after it.  The loads are unconditional, one element per register, at clamped indices
+    // (out-of-range columns and rows are dropped in the epilogue; without a bias, A[0] stands in and
+    // is not used): a branch around a load, or converting or packing the value before the
+    // epilogue, would make the wave wait for the load right here.  (The residual may alias C: this
+    // lane is the only one that writes these elements, in the epilogue.)
+    uint32_t bs_e[TN][4];            // fp16 bias bits, zero-extended
+    float sc_e[TN][4];
+    uint32_t rs_e[TN][TM][4];        // fp16 residual bits
+#pragma unroll
+    for (int a = 0; a < TN; ++a) {
+        const int nb = n0 + wn0 + a * 16 + lgrp * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int n = min(nb + i, N - 1);
+            sc_e[a][i] = 1.f;
+            if constexpr (QW) sc_e[a][i] = Ws[n];
+            bs_e[a][i] = *(bias ? bias + n : A);
+        }
+#pragma unroll
+        for (int b = 0; b < TM; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                rs_e[a][b][i] = 0u;
+                if constexpr (EPI == EPI_RESID)
+                    rs_e[a][b][i] = resid[(size_t)min(m0 + wm0 + b * 16 + lrow, M - 1) * N + min(nb + i, N - 1)];
+            }
+    }
+
     // Prologue: tiles 0 .. S-U-1 in flight (the config table requires nk >= S - U, nk % U == 0).
 #pragma unroll
     for (int s = 0; s < S - U; ++s) issue(s);
@@ -483,31 +513,16 @@ __global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restri
         lds_barrier();   // every wave is done with the last k-tile's fragments (and the k-group sums)
 #pragma unroll
         for (int a = 0; a < TN && kg == 0; ++a) {
-            const int nl = wn0 + a * 16 + lgrp * 4, nb = n0 + nl;
-            float sc[4] = {1.f, 1.f, 1.f, 1.f}, bs[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (nb + i < N) {
-                    if constexpr (QW) sc[i] = Ws[nb + i];
-                    if (bias) bs[i] = h2f(bias[nb + i]);
-                }
-            }
+            const int nl = wn0 + a * 16 + lgrp * 4;
 #pragma unroll
             for (int b = 0; b < TM; ++b) {
                 const int ml = wm0 + b * 16 + lrow;
-                uint16_t r[4] = {0, 0, 0, 0};
-                if (EPI == EPI_RESID && m0 + ml < M) {
-                    const uint16_t *rp = resid + (size_t)(m0 + ml) * N + nb;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        if (nb + i < N) r[i] = rp[i];
-                }
                 uint16_t o[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     float v = acc[a][b][i];
-                    if constexpr (QW) v = v * sc[i];
-                    o[i] = epi_out<EPI>(v + bs[i], r[i]);
+                    if constexpr (QW) v = v * sc_e[a][i];
+                    o[i] = epi_out<EPI>(v + (bias ? h2f((uint16_t)bs_e[a][i]) : 0.f), (uint16_t)rs_e[a][b][i]);
                 }
                 *reinterpret_cast<uint2 *>(ct + ml * CS + nl) =
                     uint2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
@@ -530,36 +545,16 @@ __global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restri
 #pragma unroll
     for (int a = 0; a < TN; ++a) {
         const int nb = n0 + wn0 + a * 16 + lgrp * 4;
-        float sc[4] = {1.f, 1.f, 1.f, 1.f}, bs[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (nb + i < N) {
-                if constexpr (QW) sc[i] = Ws[nb + i];
-                if (bias) bs[i] = h2f(bias[nb + i]);
-            }
-        }
 #pragma unroll
         for (int b = 0; b < TM; ++b) {
             const int m = m0 + wm0 + b * 16 + lrow;
             if (m >= M) continue;
-            uint16_t r[4] = {0, 0, 0, 0};   // residual (EPI_RESID; may alias C: same lane reads, then writes)
-            if constexpr (EPI == EPI_RESID) {
-                const uint16_t *rp = resid + (size_t)m * N + nb;
-                if (vec_store && nb + 3 < N) {
-                    const uint2 rv = *reinterpret_cast<const uint2 *>(rp);
-                    r[0] = (uint16_t)rv.x; r[1] = (uint16_t)(rv.x >> 16); r[2] = (uint16_t)rv.y; r[3] = (uint16_t)(rv.y >> 16);
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        if (nb + i < N) r[i] = rp[i];
-                }
-            }
             uint16_t o[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float v = acc[a][b][i];
-                if constexpr (QW) v = v * sc[i];
-                o[i] = epi_out<EPI>(v + bs[i], r[i]);
+                if constexpr (QW) v = v * sc_e[a][i];
+                o[i] = epi_out<EPI>(v + (bias ? h2f((uint16_t)bs_e[a][i]) : 0.f), (uint16_t)rs_e[a][b][i]);
             }
             uint16_t *dst = C + (size_t)m * N + nb;
             if (vec_store && nb + 3 < N) {
