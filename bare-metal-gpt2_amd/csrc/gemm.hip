@@ -674,13 +674,13 @@ static const GemmCfg kCfgs[] = {
     G2_DCFGU(48, 32, 3, 2, 4, 2, 2),  // 22: as 15, two k-tiles per barrier
     G2_DCFGUF(48, 32, 3, 2, 6, 2, 2), // 23: as 15, two k-tiles per barrier, 6 stages (mlp-proj)
     G2_DCFGU(48, 32, 3, 2, 4, 1, 2),  // 24: as 9, two k-tiles per barrier (QKV)
-    G2_DCFGU(48, 32, 3, 2, 6, 1, 2),  // 25: as 9, two k-tiles per barrier, 6 stages
+    G2_DCFGUF(48, 32, 3, 2, 6, 1, 2), // 25: as 9, two k-tiles per barrier, 6 stages (attn-proj)
     G2_DCFGUF(48, 64, 3, 4, 4, 1, 2), // 26: as 20, two k-tiles per barrier (fc)
     G2_DCFGU(48, 64, 3, 4, 6, 1, 2),  // 27: as 20, two k-tiles per barrier, 6 stages
     G2_DCFGU(48, 32, 3, 2, 6, 1, 3),  // 28: as 9, three k-tiles per barrier
     G2_DCFGU(48, 64, 3, 4, 6, 1, 3),  // 29: as 20, three k-tiles per barrier
     G2_DCFGU(48, 32, 3, 2, 6, 2, 3),  // 30: as 15, three k-tiles per barrier
-    G2_DCFGUF(48, 32, 3, 2, 8, 1, 4), // 31: as 9, four k-tiles per barrier (attn-proj)
+    G2_DCFGUF(48, 32, 3, 2, 8, 1, 4), // 31: as 9, four k-tiles per barrier (INT8 attn-proj)
     G2_DCFGU(48, 64, 3, 4, 8, 1, 4),  // 32: as 20, four k-tiles per barrier
     G2_DCFGUF(48, 32, 3, 2, 8, 2, 4), // 33: as 15, four k-tiles per barrier (160 KB of LDS; INT8 mlp-proj)
     G2_DCFGUF(48, 64, 3, 2, 4, 1, 2),   // 34: 6 waves, wave tile 16x32 (each widened INT8 fragment feeds 2 MFMAs)
@@ -744,7 +744,7 @@ static int pick_cfg(int M, int N, int K, bool qw = false) {
     }
     if (M > 256 && M <= 512) {
         int c = -1;
-        if (N == 768 && K == 768) c = 31;                 // attn-proj: 48x32, 6 waves, 8 stages, 4/barrier
+        if (N == 768 && K == 768) c = 25;                 // attn-proj: 48x32, 6 waves, 6 stages, 2/barrier
         else if (N == 768 && K == 3072) c = 23;           // mlp-proj: 48x32, 2 k groups, 6 stages, 2/barrier
         else if (N == 2304 && K == 768) c = 24;           // QKV: 48x32, 6 waves, 2 k-tiles/barrier
         else if (N == 3072 && K == 768) c = 26;           // fc: 48x64, 12 waves, 2 k-tiles/barrier
