@@ -68,9 +68,9 @@ __device__ __forceinline__ float slot_sum(float v) {
 //     (resid may alias C: each output is read and written by the same lane).
 template <int LPR, int CPL, int U, bool QW, bool LN = false, int EPI = EPI_NONE>
 __global__ __launch_bounds__(256) void k_gemv(uint16_t *C, const uint16_t *__restrict__ x,
-                                              const void *__restrict__ Wv, const float *__restrict__ Ws,
-                                              const uint16_t *__restrict__ bias, int N,
-                                              const uint16_t *__restrict__ ln_g, const uint16_t *__restrict__ ln_b,
+                                              const void *__restrict__ Wv, const float *Ws,
+                                              const uint16_t *bias, int N,
+                                              const uint16_t *ln_g, const uint16_t *ln_b,
                                               const uint16_t *resid) {
     constexpr int RPW = 64 / LPR;                  // row slots per wave
     constexpr int ROWB = LPR * CPL * 16;           // bytes per weight row
@@ -90,14 +90,41 @@ __global__ __launch_bounds__(256) void k_gemv(uint16_t *C, const uint16_t *__res
 
     const char *W = reinterpret_cast<const char *>(Wv);
     i32x4 wv[U][CPL];
+    // Rows past N read row N-1 (their sums are never stored): unconditional loads keep all of them
+    // in flight at once, where a branch per load would make the wave wait between them.
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int r = rbase + u * RPW;
+        const int r = min(rbase + u * RPW, N - 1);
 #pragma unroll
         for (int i = 0; i < CPL; ++i)
-            wv[u][i] = (r < N) ? *reinterpret_cast<const i32x4 *>(W + (size_t)r * ROWB + (j + LPR * i) * 16)
-                               : i32x4{0, 0, 0, 0};
+            wv[u][i] = *reinterpret_cast<const i32x4 *>(W + (size_t)r * ROWB + (j + LPR * i) * 16);
     }
+    // The rows' scale, bias and residual (and the LayerNorm parameters) are loaded with the weights,
+    // unconditionally at clamped rows (without a bias, x[0] stands in and is not used), each value
+    // in its own register until the epilogue: loaded after the reduction, they would cost a second
+    // memory round trip per launch.
+    float sc_e[U];
+    uint32_t bs_e[U], rs_e[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int r = min(rbase + u * RPW, N - 1);
+        sc_e[u] = 1.f;
+        if constexpr (QW) sc_e[u] = Ws[r];
+        bs_e[u] = *(bias ? bias + r : x);
+        rs_e[u] = 0u;
+        if constexpr (EPI == EPI_RESID) rs_e[u] = resid[r];
+    }
+    f16x8 lg[LN ? XV : 1], lb[LN ? XV : 1];
+    if constexpr (LN) {
+#pragma unroll
+        for (int v = 0; v < XV; ++v) {
+            lg[v] = *reinterpret_cast<const f16x8 *>(ln_g + xoff(v));
+            lb[v] = *reinterpret_cast<const f16x8 *>(ln_b + xoff(v));
+        }
+    }
+    // keeps the compiler from sinking those loads down to their use (no wait is implied; the
+    // pointers are not __restrict__, so the loads cannot move across this point)
+    asm volatile("" ::: "memory");
 
     if constexpr (LN) {
         constexpr float invK = 1.0f / (float)(XV * 8 * LPR);
@@ -117,12 +144,9 @@ __global__ __launch_bounds__(256) void k_gemv(uint16_t *C, const uint16_t *__res
             }
         const float rstd = 1.0f / sqrtf(slot_sum<LPR>(sq) * invK + GPT2_LN_EPS);
 #pragma unroll
-        for (int v = 0; v < XV; ++v) {
-            const f16x8 g = *reinterpret_cast<const f16x8 *>(ln_g + xoff(v));
-            const f16x8 b = *reinterpret_cast<const f16x8 *>(ln_b + xoff(v));
+        for (int v = 0; v < XV; ++v)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) xr[v][e] = (f16)(((float)xr[v][e] - mean) * rstd * (float)g[e] + (float)b[e]);
-        }
+            for (int e = 0; e < 8; ++e) xr[v][e] = (f16)(((float)xr[v][e] - mean) * rstd * (float)lg[v][e] + (float)lb[v][e]);
     }
 
 #pragma unroll
@@ -135,14 +159,13 @@ __global__ __launch_bounds__(256) void k_gemv(uint16_t *C, const uint16_t *__res
             else acc = dot8(wv[u][i], xr[i], acc);
         }
         acc = slot_sum<LPR>(acc);
-        if (j == 0 && r < N) {
-            float v = acc;
-            if constexpr (QW) v *= Ws[r];
-            if (bias) v += h2f(bias[r]);
-            if constexpr (EPI == EPI_GELU) v = gelu_tanh(v);
-            if constexpr (EPI == EPI_RESID) v += h2f(resid[r]);
-            C[r] = f2h(v);
-        }
+        // the epilogue runs on every lane (the values were loaded for every lane), one lane stores
+        float v = acc;
+        if constexpr (QW) v *= sc_e[u];
+        if (bias) v += h2f((uint16_t)bs_e[u]);
+        if constexpr (EPI == EPI_GELU) v = gelu_tanh(v);
+        if constexpr (EPI == EPI_RESID) v += h2f((uint16_t)rs_e[u]);
+        if (j == 0 && r < N) C[r] = f2h(v);
     }
 }
 
