@@ -84,15 +84,14 @@ __global__ __launch_bounds__(64 * AP_W) void k_attn_prefill_mfma(uint16_t *__res
     }
     if (qi >= nb) return;                      // the grid is rounded up (whole work-group leaves)
     const int q0 = (nb - 1 - qi) * AP_QB;
-    if (Kc) {
-        // The prefill's K/V cache rows of this block's positions and head, one 16-byte chunk per
-        // thread (16 positions x 8 chunks for K, the same for V), into [H][maxT][D] of the layer.
-        static_assert(2 * AP_QB * (D / 8) == 64 * AP_W, "one chunk per thread");
-        const int t = q0 + ((threadIdx.x >> 3) & (AP_QB - 1)), d8 = (threadIdx.x & 7) * 8, v = threadIdx.x >> 7;
-        if (t < T)
-            *reinterpret_cast<f16x8 *>((v ? Vc : Kc) + ((size_t)h * maxT + t) * D + d8) =
-                *reinterpret_cast<const f16x8 *>(qkv + (size_t)t * S3 + (v ? 2 * E : E) + h * D + d8);
-    }
+    // The prefill's K/V cache rows of this block's positions and head, one 16-byte chunk per thread
+    // (16 positions x 8 chunks for K, the same for V), into [H][maxT][D] of the layer.  The chunk is
+    // loaded here, before the queries and keys (unconditionally, at a clamped row), and stored at
+    // the end: storing it right after its load would make the wave wait a memory round trip before
+    // issuing any attention load.
+    static_assert(2 * AP_QB * (D / 8) == 64 * AP_W, "one chunk per thread");
+    const int ft = q0 + ((threadIdx.x >> 3) & (AP_QB - 1)), fd8 = (threadIdx.x & 7) * 8, fv = threadIdx.x >> 7;
+    const f16x8 fill = *reinterpret_cast<const f16x8 *>(qkv + (size_t)min(ft, T - 1) * S3 + (fv ? 2 * E : E) + h * D + fd8);
     const int qlast = min(q0 + AP_QB, T) - 1;
     const int nc = qlast / AP_CK + 1;          // chunks over keys [0, qlast]; chunk start <= q0
     const int q = q0 + jq;                     // this lane's query (q >= T: computed, not stored)
@@ -229,6 +228,8 @@ __global__ __launch_bounds__(64 * AP_W) void k_attn_prefill_mfma(uint16_t *__res
         L += lw[u] * f;
         acc += mrg_o[u][wave][lane] * f;
     }
+    if (Kc && ft < T)   // every wave, including those with no chunk
+        *reinterpret_cast<f16x8 *>((fv ? Vc : Kc) + ((size_t)h * maxT + ft) * D + fd8) = fill;
     if (q < T) {
         const float inv = 1.0f / L;
         const uint2 pk = {(uint32_t)f2h(acc[0] * inv) | ((uint32_t)f2h(acc[1] * inv) << 16),
