@@ -864,3 +864,11 @@ extern "C" void gpt2_tune_gemm_run(int cfg, gpt2_half *C, const gpt2_half *A, co
     if (gemm_args("gpt2_tune_gemm_run", C, A, W, M, N, K)) return;
     gemm(C, A, W, Ws, bias, M, N, K, Ws != nullptr, cfg);
 }
+// The prefill's fused-epilogue GEMMs (epi 1: gelu_new, 2: + resid, which may be C itself), for
+// tests: returns 1 when a fused kernel ran, 0 when none covers the call (the prefill then runs the
+// plain GEMM and the separate elementwise kernel).
+extern "C" int gpt2_tune_gemm_fused(gpt2_half *C, const gpt2_half *A, const void *W, const float *Ws,
+                                    const gpt2_half *bias, int M, int N, int K, int epi, const gpt2_half *resid) {
+    if (gemm_args("gpt2_tune_gemm_fused", C, A, W, M, N, K)) return 0;
+    return gemm_fused(C, A, W, Ws, bias, M, N, K, Ws != nullptr, epi, resid) ? 1 : 0;
+}

@@ -261,3 +261,36 @@ def test_dispatch_rule(pkg, L):
     assert not np.array_equal(out[("int8", "q")], out[("int8", "null")])
     for key in (("int8", "null"), ("flash", "q"), ("flash", "null")):
         tol_check(out[key], ref16)
+
+
+@pytest.mark.parametrize("kind", ["fp16", "int8"])
+@pytest.mark.parametrize("M,N,K", [(512, 768, 768), (512, 3072, 768), (200, 768, 3072), (33, 772, 768), (65, 770, 768)])
+def test_fused_epilogues(pkg, L, kind, M, N, K):
+    """The prefill's fused-epilogue GEMMs (forward_cuda.cu:99-105 folded into the GEMM: gelu_new of
+    fp16(A.W^T + b), and fp16(resid + fp16(A.W^T + b)) with resid == C in place and in a separate
+    buffer) against the oracle's matmul, gelu and add on the same fp16 values, at the trunk shapes,
+    ragged M, and N with and without 8-byte C rows (the staged epilogue).  Bar as above."""
+    rng = np.random.default_rng(M * 7 + N + K)
+    A = f16v(rng, (M, K), 1.0)
+    b = f16v(rng, N, 0.01)
+    R = f16v(rng, (M, N), 1.0)
+    if kind == "int8":
+        q, s, _ = oracle.quantize_fp16_view(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+        Wd = oracle.dequantize(q, s)
+        dW, ds = pkg.Dev.from_numpy(q), pkg.Dev.from_numpy(s)
+    else:
+        Wd = f16v(rng, (N, K), 0.02)
+        dW, ds = dev16(pkg, Wd), None
+    base = oracle.fp16_view(oracle.matmul(A, Wd, b))          # fp16(A.W^T + b)
+    dA, db = dev16(pkg, A), dev16(pkg, b)
+    for epi, want in ((1, oracle.fp16_view(oracle.gelu(base))), (2, oracle.fp16_view(R + base))):
+        for in_place in ((False, True) if epi == 2 else (False,)):
+            dC = dev16(pkg, R) if in_place else pkg.Dev(M * N * 2)
+            dR = dC if in_place else dev16(pkg, R)
+            ran = L.gpt2_tune_gemm_fused(dC.ptr, dA.ptr, dW.ptr, ds.ptr if ds is not None else None, db.ptr,
+                                         M, N, K, epi, dR.ptr if epi == 2 else None)
+            L.gpt2_sync()
+            pkg.check("fused gemm")
+            assert ran == 1, (kind, M, N, K, epi)
+            got = oracle.f16_to_f32(dC.numpy(np.uint16, (M, N)))
+            tol_check(got, want)
