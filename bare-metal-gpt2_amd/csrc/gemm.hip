@@ -746,7 +746,7 @@ static int pick_cfg(int M, int N, int K, bool qw = false) {
         int c = -1;
         if (N == 768 && K == 768) c = 25;                 // attn-proj: 48x32, 6 waves, 6 stages, 2/barrier
         else if (N == 768 && K == 3072) c = 23;           // mlp-proj: 48x32, 2 k groups, 6 stages, 2/barrier
-        else if (N == 2304 && K == 768) c = 24;           // QKV: 48x32, 6 waves, 2 k-tiles/barrier
+        else if (N == 2304 && K == 768) c = 35;           // QKV: 48x32, 3 waves (16x32 wave tiles), 2 k-tiles/barrier
         else if (N == 3072 && K == 768) c = 26;           // fc: 48x64, 12 waves, 2 k-tiles/barrier
         if (c >= 0 && cfg_fits(c, K)) return c;
     }
