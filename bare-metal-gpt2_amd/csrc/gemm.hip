@@ -695,9 +695,10 @@ static const GemmCfg kCfgs[] = {
     G2_CFG(64, 32, 64, 2, 2, 6),    // 42: wave tile 32x16
     G2_CFG(32, 64, 64, 1, 4, 6),    // 43: wave tile 32x16
     G2_CFG(128, 128, 64, 2, 2, 2),  // 44: wave tile 64x64
+    G2_DCFGUF(48, 32, 3, 1, 4, 4, 2),   // 45: four k groups of 3 waves, 16x32 wave tiles (INT8 mlp-proj)
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
-static_assert(sizeof(kCfgs) / sizeof(kCfgs[0]) == 45, "the pick table names configs by index");
+static_assert(sizeof(kCfgs) / sizeof(kCfgs[0]) == 46, "the pick table names configs by index");
 
 // Any K % 8 == 0 (int8: K % 16 == 0): predicated loads, one k-tile of prefetch.
 #define G2_GCFG(BN, BM, WN, WM) \
@@ -734,12 +735,13 @@ static int pick_cfg(int M, int N, int K, bool qw = false) {
         // INT8 weights (widened to fp16 as fragments are read), picked the same way on an INT8 step:
         // QKV and fc take 16x32 wave tiles (3 waves), so each widened W fragment feeds two MFMAs and
         // fewer waves widen the same rows (400.5 us per step, against 425.4 with the fp16 picks'
-        // shapes and 467.3 with the fp16 table itself).
+        // shapes and 467.3 with the fp16 table itself); mlp-proj (K=3072) splits K over four groups
+        // of such waves (367.6 against 381.2 us with two groups of 6 waves).
         int c = -1;
         if (N == 2304 && K == 768) c = 35;                // QKV: 48x32, 3 waves, 2 k-tiles/barrier
         else if (N == 768 && K == 768) c = 31;            // attn-proj: 48x32, 8 stages, 4/barrier
         else if (N == 3072 && K == 768) c = 35;           // fc: as QKV
-        else if (N == 768 && K == 3072) c = 33;           // mlp-proj: 48x32, 2 k groups, 8 stages, 4/barrier
+        else if (N == 768 && K == 3072) c = 45;           // mlp-proj: 48x32, 4 k groups of 3 waves, 2/barrier
         if (c >= 0 && cfg_fits(c, K)) return c;
     }
     if (M > 256 && M <= 512) {
