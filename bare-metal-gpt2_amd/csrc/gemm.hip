@@ -696,9 +696,10 @@ static const GemmCfg kCfgs[] = {
     G2_CFG(32, 64, 64, 1, 4, 6),    // 43: wave tile 32x16
     G2_CFG(128, 128, 64, 2, 2, 2),  // 44: wave tile 64x64
     G2_DCFGUF(48, 32, 3, 1, 4, 4, 2),   // 45: four k groups of 3 waves, 16x32 wave tiles (INT8 mlp-proj)
+    G2_DCFG(128, 64, 4, 2, 2),          // 46: as 1, double-buffered (49 KB of LDS: three work-groups per CU)
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
-static_assert(sizeof(kCfgs) / sizeof(kCfgs[0]) == 46, "the pick table names configs by index");
+static_assert(sizeof(kCfgs) / sizeof(kCfgs[0]) == 47, "the pick table names configs by index");
 
 // Any K % 8 == 0 (int8: K % 16 == 0): predicated loads, one k-tile of prefetch.
 #define G2_GCFG(BN, BM, WN, WM) \
@@ -752,8 +753,10 @@ static int pick_cfg(int M, int N, int K, bool qw = false) {
         else if (N == 3072 && K == 768) c = 26;           // fc: 48x64, 12 waves, 2 k-tiles/barrier
         if (c >= 0 && cfg_fits(c, K)) return c;
     }
-    // Vocabulary-sized N (the tied head, 50257 rows of W): many tiles per CU, bound by L2 bytes per
-    // FLOP, where large tiles win (M=512: 128x64 83 us, 256x128 88, 128x128 94, 48-row tiles >= 135).
+    // Vocabulary-sized N (the tied head, 50257 rows of W): many tiles per CU, where large tiles win
+    // on L2 bytes per FLOP (M=512: 128x64 83 us, 256x128 88, 128x128 94, 48-row tiles >= 135) and
+    // the 128x64 tile double-buffered (three work-groups per CU) beats its 3-stage form (64 vs 74 us).
+    if (N >= 16384 && M > 32 && cfg_fits(46, K)) return 46;
     if (N >= 16384 && M > 32 && cfg_fits(1, K)) return 1;
     const int order[] = {6, 0, 5, 2, 3, 8};
     int last = -1;
