@@ -697,9 +697,10 @@ static const GemmCfg kCfgs[] = {
     G2_CFG(128, 128, 64, 2, 2, 2),  // 44: wave tile 64x64
     G2_DCFGUF(48, 32, 3, 1, 4, 4, 2),   // 45: four k groups of 3 waves, 16x32 wave tiles (INT8 mlp-proj)
     G2_DCFG(128, 64, 4, 2, 2),          // 46: as 1, double-buffered (49 KB of LDS: three work-groups per CU)
+    G2_DCFGUF(32, 32, 1, 2, 4, 4, 1),   // 47: as 14 (four k groups of 2 waves), with the fused epilogues
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
-static_assert(sizeof(kCfgs) / sizeof(kCfgs[0]) == 47, "the pick table names configs by index");
+static_assert(sizeof(kCfgs) / sizeof(kCfgs[0]) == 48, "the pick table names configs by index");
 
 // Any K % 8 == 0 (int8: K % 16 == 0): predicated loads, one k-tile of prefetch.
 #define G2_GCFG(BN, BM, WN, WM) \
@@ -756,6 +757,9 @@ static int pick_cfg(int M, int N, int K, bool qw = false) {
     // Vocabulary-sized N (the tied head, 50257 rows of W): many tiles per CU, where large tiles win
     // on L2 bytes per FLOP (M=512: 128x64 83 us, 256x128 88, 128x128 94, 48-row tiles >= 135) and
     // the 128x64 tile double-buffered (three work-groups per CU) beats its 3-stage form (64 vs 74 us).
+    // Few rows and a long K (mlp-proj of a 64-token prefill: 24 x 2 tiles of 32x32): four k groups per
+    // tile keep more waves busy (M=64: 6.9 us against 9+ us with one group).
+    if (M <= 64 && K >= 2048 && N <= 4096 && cfg_fits(47, K)) return 47;
     if (N >= 16384 && M > 32 && cfg_fits(46, K)) return 46;
     if (N >= 16384 && M > 32 && cfg_fits(1, K)) return 1;
     const int order[] = {6, 0, 5, 2, 3, 8};
