@@ -24,11 +24,10 @@ struct PDArgs {
     uint16_t *kv;                     // [L][K|V][H][maxT][D]
     int maxT;
     uint16_t *logits;                 // [V] fp16
-    int *state;                       // {token, pos, epoch}
+    int *state;                       // {token, pos, epoch, err, spin}
     int *tokens;                      // tokens[pos+1] = next
     uint64_t *ll;                     // exchange arena, LL_WORDS words
     int *err;                         // nonzero after a poll timed out
-    int spin;                         // poll rounds before a work-group gives up
     unsigned long long *trace;        // optional: [G][128] phase times (100 MHz clock)
 };
 
@@ -42,5 +41,6 @@ bool persist_plan(PDPlan &p, const GPT2Backend *be, const GPT2WeightsGPU *w, GPT
                   int *state, int *tokens, uint64_t *ll, int *err);
 void persist_launch(const PDPlan &p, hipStream_t s);
 size_t persist_ll_bytes();
+int persist_spin();   // poll rounds before a work-group gives up (state[4] of new graphs and of each set)
 
 }  // namespace g2

@@ -400,9 +400,12 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     uint32_t *xout = reinterpret_cast<uint32_t *>(lds + LDS_MISC + 112);   // RP x words, one store
     static_assert(64 + 2 * RF <= 96 && 112 + 4 * RP <= 512, "LDS misc layout");
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wg = blockIdx.x;
+    // wave < 4 made explicit (PD_T = 256): a wave's share of GEMV rows (wave + 4j < ROWS) is then
+    // known at compile time, with no branch around the row dot products ahead of their reductions.
+    const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, wg = blockIdx.x;
     const int token = a.state[0], pos = a.state[1];
     const uint32_t epoch = (uint32_t)a.state[2];
+    const int spin = a.state[4];   // poll rounds before giving up
     if ((unsigned)pos >= (unsigned)a.maxT || (unsigned)token >= (unsigned)PD_V) return;   // uniform
     auto seq = [&](int phase) { return epoch * 64u + (uint32_t)phase; };
     auto mark = [&](int phase) {
@@ -414,7 +417,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     const size_t hstride = (size_t)a.maxT * PD_D;
 
     auto read_x = [&](uint32_t flag, unsigned long long *dbg = nullptr) {
-        return ll_read<XR>(LX, PD_E, flag, a.err, a.spin, wflag, x_word,
+        return ll_read<XR>(LX, PD_E, flag, a.err, spin, wflag, x_word,
                           [&](int i, uint32_t d) { xs[i] = __builtin_bit_cast(f16, (uint16_t)d); }, dbg);
     };
 
@@ -546,20 +549,20 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 f16x8 q[8];
                 load_q(q, reinterpret_cast<const uint16_t *>(qkvh));
                 const bool on = w0 + lane < w1;
-                float sv = -INFINITY;
-                if (on) {
-                    float d0 = 0.f, d1 = 0.f;
+                // Every lane computes its dot product (kr is zero past w1) and the out-of-range lanes
+                // are masked by a select afterwards: no lane-divergent branch precedes the DPP
+                // reduction, so every lane of the row holds a value the select wrote.
+                float d0 = 0.f, d1 = 0.f;
 #pragma unroll
-                    for (int c = 0; c < 8; ++c)
+                for (int c = 0; c < 8; ++c)
 #pragma unroll
-                        for (int t = 0; t < 4; t += 2) {
-                            d0 = __builtin_amdgcn_fdot2(f16x2{q[c][2 * t], q[c][2 * t + 1]}, f16x2{kr[c][2 * t], kr[c][2 * t + 1]},
-                                                        d0, false);
-                            d1 = __builtin_amdgcn_fdot2(f16x2{q[c][2 * t + 2], q[c][2 * t + 3]},
-                                                        f16x2{kr[c][2 * t + 2], kr[c][2 * t + 3]}, d1, false);
-                        }
-                    sv = (d0 + d1) * 0.125f;
-                }
+                    for (int t = 0; t < 4; t += 2) {
+                        d0 = __builtin_amdgcn_fdot2(f16x2{q[c][2 * t], q[c][2 * t + 1]}, f16x2{kr[c][2 * t], kr[c][2 * t + 1]},
+                                                    d0, false);
+                        d1 = __builtin_amdgcn_fdot2(f16x2{q[c][2 * t + 2], q[c][2 * t + 3]},
+                                                    f16x2{kr[c][2 * t + 2], kr[c][2 * t + 3]}, d1, false);
+                    }
+                const float sv = on ? (d0 + d1) * 0.125f : -INFINITY;
                 m_w = wave_max_u(sv);   // finite: key w0 is in range
                 const float pv = on ? __expf(sv - m_w) : 0.f;
                 pl[wave][(lane & 7) * 8 + (lane >> 3)] = pv;
@@ -670,7 +673,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
         for (int l = 0; l < GPT2_N_LAYER; ++l) {
             // ---- P: combine the attention words, proj rows, + bias + residual
             constexpr int NA = PD_NA * PD_PW;
-            if (!ll_read<(NA + PD_T - 1) / PD_T>(LA, NA, seq(4 * l), a.err, a.spin, wflag, at_word,
+            if (!ll_read<(NA + PD_T - 1) / PD_T>(LA, NA, seq(4 * l), a.err, spin, wflag, at_word,
                                                  [&](int i, uint32_t d) { part[i] = __uint_as_float(d); }))
                 return;
             mark(64 + 4 * l + 1);
@@ -738,7 +741,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 ll_st(LHd + hd_word(g * RF / 2 + tid), (uint32_t)hout[2 * tid] | ((uint32_t)hout[2 * tid + 1] << 16), seq(4 * l + 2));
             mark(4 * l + 2);
             // ---- M: mlp-proj rows [g*RM, +RM) over gelu(fc), + bias + residual
-            if (!ll_read<PD_F / 2 / PD_T>(LHd, PD_F / 2, seq(4 * l + 2), a.err, a.spin, wflag, hd_word,
+            if (!ll_read<PD_F / 2 / PD_T>(LHd, PD_F / 2, seq(4 * l + 2), a.err, spin, wflag, hd_word,
                                           [&](int i, uint32_t d) {
                                               hs[2 * i] = __builtin_bit_cast(f16, (uint16_t)(d & 0xffff));
                                               hs[2 * i + 1] = __builtin_bit_cast(f16, (uint16_t)(d >> 16));
@@ -870,7 +873,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     if (wg != 0) return;
     // work-group 0: argmax over the candidates, advance the state
     uint32_t *cands = reinterpret_cast<uint32_t *>(lds + LY::CANDS);
-    if (!ll_read<(PD_G + PD_T - 1) / PD_T>(LC, PD_G, seq(ph), a.err, a.spin, wflag, cand_word,
+    if (!ll_read<(PD_G + PD_T - 1) / PD_T>(LC, PD_G, seq(ph), a.err, spin, wflag, cand_word,
                                           [&](int i, uint32_t d) { cands[i] = d; }))
         return;
     {
@@ -909,8 +912,20 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
 static int g_pd_spin = PD_SPIN;
 static unsigned long long *g_pd_trace = nullptr;
 
+// The step's work-groups wait on each other's words, so all PD_G of them must be resident at once:
+// the device must hold PD_G of them (one per CU with this LDS footprint) side by side.
+static bool persist_fits(bool q8) {
+    int dev = 0, ncu = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
+    const hipError_t e = q8 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_decode_persist<true>, PD_T, 0)
+                            : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_decode_persist<false>, PD_T, 0);
+    return e == hipSuccess && (long)per * ncu >= PD_G;
+}
+
 // Builds the step's argument block; returns false when the backend or weights need the
-// multi-kernel step (the caller falls back to it).
+// multi-kernel step (the caller falls back to it), or when the device cannot hold every
+// work-group of the step at once.
 bool persist_plan(PDPlan &p, const GPT2Backend *be, const GPT2WeightsGPU *w, GPT2KVCache *kv, uint16_t *logits,
                   int *state, int *tokens, uint64_t *ll, int *err) {
     if (be->gemv != gpt2_gemv_fp16) return false;
@@ -944,6 +959,7 @@ bool persist_plan(PDPlan &p, const GPT2Backend *be, const GPT2WeightsGPU *w, GPT
     if (nq != 0 && nq != 4 * GPT2_N_LAYER) return false;
     if (kv->maxT > GPT2_N_CTX) return false;   // an attention wave holds at most 64 keys
     p.q8 = nq != 0;
+    if (!persist_fits(p.q8)) return false;
     a.wte = w->wte;
     a.wpe = w->wpe;
     a.lnf_g = w->lnf_g;
@@ -958,7 +974,6 @@ bool persist_plan(PDPlan &p, const GPT2Backend *be, const GPT2WeightsGPU *w, GPT
     a.tokens = tokens;
     a.ll = ll;
     a.err = err;
-    a.spin = g_pd_spin;
     a.trace = g_pd_trace;
     return true;
 }
@@ -970,10 +985,13 @@ void persist_launch(const PDPlan &p, hipStream_t s) {
 
 size_t persist_ll_bytes() { return (size_t)LL_WORDS * 8; }
 
+int persist_spin() { return g_pd_spin; }
+
 }  // namespace g2
 
-// Tuning / test hook: poll rounds before a persistent step gives up, for graphs created afterwards
-// (< 0 restores the default; 0 gives up at the first poll that finds a word missing).  A tiny value
+// Tuning / test hook: poll rounds before a persistent step gives up, for the steps of graphs created
+// or set (gpt2_decode_graph_set) afterwards (< 0 restores the default; 0 gives up at the first poll
+// that finds a word missing).  A tiny value
 // forces the timeout path with every kernel still exiting normally.
 extern "C" void gpt2_tune_decode_spin(int rounds) { g2::g_pd_spin = rounds >= 0 ? rounds : g2::PD_SPIN; }
 // Profiling hook: graphs created afterwards record, per work-group, the end time of every phase of

@@ -413,7 +413,7 @@ struct GPT2DecodeGraph {
     hipStream_t stream;
     hipGraph_t graph;       // one step (multi-kernel) or PERSIST_CHUNK steps (persistent)
     hipGraphExec_t exec;
-    int *state;       // device {token, pos, epoch, error}
+    int *state;       // device {token, pos, epoch, error, poll limit}
     GPT2KVCache *kv;
     int host_pos;     // position the next replay consumes, tracked on the host
     int mode;         // GPT2_DECODE_MULTI or GPT2_DECODE_PERSISTENT
@@ -442,9 +442,9 @@ extern "C" GPT2DecodeGraph *gpt2_decode_graph_create_mode(const GPT2Backend *be,
     g->host_pos = kv->len;
     g->mode = GPT2_DECODE_MULTI;
     if (hipStreamCreate(&g->stream) != hipSuccess) { g->stream = nullptr; graph_free(g); set_error(E_STATE, "hipStreamCreate"); return nullptr; }
-    g->state = (int *)gpt2_dmalloc(4 * sizeof(int));
+    g->state = (int *)gpt2_dmalloc(8 * sizeof(int));
     if (!g->state) { graph_free(g); return nullptr; }
-    const int init[4] = {0, kv->len, 1, 0};   // epoch 1: the zeroed exchange arena holds flag 0
+    const int init[5] = {0, kv->len, 1, 0, persist_spin()};   // epoch 1: the zeroed exchange arena holds flag 0
     if (hipMemcpy(g->state, init, sizeof(init), hipMemcpyHostToDevice) != hipSuccess) {
         graph_free(g);
         set_error(E_STATE, "decode graph state");
@@ -495,8 +495,20 @@ extern "C" int gpt2_decode_graph_mode(const GPT2DecodeGraph *g) { return g ? g->
 
 extern "C" int gpt2_decode_graph_set(GPT2DecodeGraph *g, int token, int pos) {
     if (!g || token < 0 || token >= GPT2_VOCAB || pos < 0 || pos >= g->kv->maxT) { set_error(E_ARG, "gpt2_decode_graph_set"); return 1; }
-    const int st[2] = {token, pos};
-    hipError_t e = hipMemcpyAsync(g->state, st, sizeof(st), hipMemcpyHostToDevice, g->stream);
+    // {token, pos, epoch + 1, 0, poll limit}: the error word of a step that timed out is cleared,
+    // and the next epoch makes every exchange word that step left behind stale (its sequence numbers
+    // can no longer match a poll).
+    int st[5];
+    hipError_t e = hipMemcpyAsync(st, g->state, sizeof(st), hipMemcpyDeviceToHost, g->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g->stream);
+    if (e == hipSuccess) {
+        st[0] = token;
+        st[1] = pos;
+        st[2] += 1;
+        st[3] = 0;
+        st[4] = persist_spin();
+        e = hipMemcpyAsync(g->state, st, sizeof(st), hipMemcpyHostToDevice, g->stream);
+    }
     if (e == hipSuccess) e = hipStreamSynchronize(g->stream);
     if (e != hipSuccess) { set_error((int)e, "gpt2_decode_graph_set"); return (int)e; }
     g->host_pos = pos;

@@ -249,10 +249,11 @@ def bench_gemv(B):
                    "cold_frac_of_8TBs": round(algo / (ms_cold * 1e-3) / 8e12, 3),
                    "warm_us": round(ms_warm * 1e3, 3), "warm_GBs": round(algo / (ms_warm * 1e-3) / 1e9, 1)}
     big.free()
-    # fp16 tied head: [1x768] . [768x50257], 77.3 MB
+    # fp16 tied head: [1x768] . [768x50257], 77.3 MB; cold rotates >= 600 MB of copies (8), well past
+    # the 256 MB MALL
     N, K = VOCAB, 768
     algo = 2 * N * K + 2 * K + 2 * N
-    R = 4
+    R = copies_for(2 * N * K)
     big = B.empty(R * N * K * 2)
     head = f16(rng, (N, K), 0.02)
     for r in range(R):
@@ -260,7 +261,7 @@ def bench_gemv(B):
     ms_cold, _ = B.run_ops([B.op(2, y.ptr, x768.ptr, big.at(r * N * K * 2), None, None, 1, N, K) for r in range(R)], 1, 10)
     ms_cold /= R
     ms_warm, _ = B.run_ops([B.op(2, y.ptr, x768.ptr, big.ptr, None, None, 1, N, K)], 10, 200)
-    head_res = {"N": N, "K": K, "bytes": algo, "cold_us": round(ms_cold * 1e3, 2),
+    head_res = {"N": N, "K": K, "bytes": algo, "copies": R, "cold_us": round(ms_cold * 1e3, 2),
                 "cold_GBs": round(algo / (ms_cold * 1e-3) / 1e9, 1), "warm_us": round(ms_warm * 1e3, 2),
                 "warm_GBs": round(algo / (ms_warm * 1e-3) / 1e9, 1)}
     big.free()
@@ -505,8 +506,84 @@ def bench_decode(B, steady_reps=64):
     return res
 
 
+# ------------------------------------------------------------------------------ measured ceilings
+def measured_peaks(B, cus):
+    """This box's ceilings, measured in the same run beside the datasheet peaks (the role of
+    bench/microbench.cu:69-377 in the reference): the HBM read stream over 4 GiB (16x the 256 MB
+    MALL, so every byte comes from HBM) and the fp16 MFMA issue loop (v_mfma_f32_16x16x32_f16, eight
+    independent accumulators per wave, one work-group of four waves per CU)."""
+    L = B.L
+    nbytes = 4 << 30
+    buf = B.pkg.Dev(nbytes)
+    L.gpt2_memset(buf.ptr, 1, nbytes)
+    ms = C.c_float()
+    if L.gpt2_bench_read(buf.ptr, nbytes, 5, C.byref(ms)):
+        B.pkg.check("gpt2_bench_read")
+    read_gbs = nbytes / (ms.value * 1e-3) / 1e9
+    buf.free()
+    blocks, iters = 4 * cus, 20000
+    if L.gpt2_bench_mfma(blocks, iters, C.byref(ms)):
+        B.pkg.check("gpt2_bench_mfma")
+    mfma_tflops = blocks * 4.0 * iters * 8 * (16 * 16 * 32 * 2) / (ms.value * 1e-3) / 1e12
+    return {"hbm_read_GBs": round(read_gbs, 1), "hbm_read_bytes": nbytes,
+            "mfma_fp16_tflops": round(mfma_tflops, 1), "mfma_loop": f"{blocks} work-groups x 4 waves x {iters} x 8 "
+            "v_mfma_f32_16x16x32_f16", "datasheet": {"hbm_GBs": PEAK_HBM_GBS, "mfma_fp16_tflops": PEAK_FP16_TFLOPS}}
+
+
+def guard_legs(out, read_gbs):
+    """The reference's bug line (bench/correctness_cuda.cu:261-270): a bandwidth figure above the
+    achieved read stream cannot be HBM.  Every leg this line calls cold (HBM) is checked against the
+    measured read stream and listed under "suspicious" when it exceeds it; the warm legs (weights held
+    in the 256 MB MALL) are listed with their ratio, labelled as MALL-resident, never as HBM."""
+    cold, warm = [], []
+    g = out.get("gemv_int8", {})
+    for name, r in g.items():
+        if "cold_GBs" in r:
+            cold.append((f"gemv_int8.{name}.cold_GBs", r["cold_GBs"]))
+        if "warm_GBs" in r:
+            warm.append((f"gemv_int8.{name}.warm_GBs", r["warm_GBs"]))
+    if "trunk_chain_48" in g:
+        warm.append(("gemv_int8.trunk_chain_48.GBs", g["trunk_chain_48"]["GBs"]))
+    h = out.get("head_gemv_fp16")
+    if h:
+        cold.append(("head_gemv_fp16.cold_GBs", h["cold_GBs"]))
+        warm.append(("head_gemv_fp16.warm_GBs", h["warm_GBs"]))
+    d = out.get("decode")
+    if d:
+        warm.append(("decode.step_GBs_at_512", d["step_GBs_at_512"]))
+    sus = [{"leg": k, "GBs": v, "over_read_stream": round(v / read_gbs, 3)} for k, v in cold if v > read_gbs]
+    return {"read_stream_GBs": read_gbs, "suspicious": sus,
+            "cold_frac_of_read_stream": {k: round(v / read_gbs, 3) for k, v in cold},
+            "warm_mall_frac_of_read_stream": {k: round(v / read_gbs, 3) for k, v in warm}}
+
+
 # ------------------------------------------------------------------------------ CPU baseline
-def cpu_baseline(budget_s=12.0):
+def host_cpu():
+    """nproc, the CPUs this process may run on, and the CPU model name (lscpu, else /proc/cpuinfo)."""
+    model = None
+    try:
+        import subprocess
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in txt.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, ValueError, Exception):
+        pass
+    return {"nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)), "model": model or cpu_model()}
+
+
+def omp_set_threads(n):
+    try:
+        C.CDLL("libgomp.so.1").omp_set_num_threads(int(n))
+        return True
+    except OSError:
+        return False
+
+
+def cpu_baseline(budget_s=12.0, one_thread_s=6.0):
+    """The reference's CPU matmul on the four GEMM shapes at M=512 (`value`: on OMP_NUM_THREADS
+    threads, the CPU share this GPU's box gives one process), then a shorter sample on one thread."""
     import oracle
     threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
     rng = np.random.default_rng(99)
@@ -527,10 +604,29 @@ def cpu_baseline(budget_s=12.0):
         if time.perf_counter() - t0 > budget_s:
             break
     dt = time.perf_counter() - t0
+    # one thread: GEMMs of the same set, one after another, while the shorter budget lasts
+    one = None
+    if omp_set_threads(1):
+        fl1, n1, t1 = 0.0, 0, time.perf_counter()
+        while True:
+            name, N, K = GEMM_SET[n1 % len(GEMM_SET)]
+            W, b = Ws[n1 % len(GEMM_SET)]
+            mm(Xf if K == 3072 else X, W, b)
+            fl1 += 2.0 * M_PREFILL * N * K
+            n1 += 1
+            if time.perf_counter() - t1 > one_thread_s:
+                break
+        d1 = time.perf_counter() - t1
+        omp_set_threads(threads)
+        one = {"value": round(fl1 / d1 / 1e12, 6), "cores": 1,
+               "sample": f"{n1} GEMMs of the set in order, {fl1 / 1e9:.2f} GFLOP, {d1:.1f} s"}
     return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
             "kind": "reference" if use_ref else "port",
             "sample": f"{sets} x the 4-GEMM set at M=512 (one layer of the workload, {flops / sets / 1e9:.3f} GFLOP"
-                      f" per set), fp32 storage / double accumulation, {dt:.1f} s"}
+                      f" per set), fp32 storage / double accumulation, {dt:.1f} s",
+            "one_thread": one, "host": host_cpu(),
+            "threads_note": "cores = OMP_NUM_THREADS, the CPU share of one GPU on this pool's boxes (16); nproc "
+                            "counts the whole host"}
 
 
 def cpu_decode_baseline(budget_s=8.0):
@@ -575,8 +671,9 @@ def main():
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the matmul path "
               "would shard by output rows (each GPU a slice of N), but no multi-GPU run is part of it.", file=sys.stderr)
         sys.exit(2)
-    cpu_threads = max(1, min(16, os.cpu_count() or 1))
-    os.environ.setdefault("OMP_NUM_THREADS", str(cpu_threads))
+    # The GPU boxes give one GPU's process a 16-thread CPU share and export OMP_NUM_THREADS=16; where
+    # it is not set, use every CPU this process may run on.
+    os.environ.setdefault("OMP_NUM_THREADS", str(max(1, len(os.sched_getaffinity(0)))))
 
     import __graft_entry__
     pkg = __graft_entry__.load_package()
@@ -611,6 +708,11 @@ def main():
            "gemm_set_graph_replay": {"us_per_step": round(ms_graph * 1e3, 2),
                                      "tflops": round(flops_step / (ms_graph * 1e-3) / 1e12, 2)}}
     B.keep.clear()
+    peaks = measured_peaks(B, cus.value)
+    out["measured_peaks"] = peaks
+    roofline["peak_measured"] = peaks["mfma_fp16_tflops"]
+    roofline["frac_of_measured"] = round(roofline["achieved"] / peaks["mfma_fp16_tflops"], 4)
+    log(f"measured peaks: {peaks}")
     if not args.no_extras:
         gemv, head = bench_gemv(B)
         B.keep.clear()
@@ -629,6 +731,9 @@ def main():
             out["decode"] = bench_decode(B)
             B.keep.clear()
             log(f"decode: {out['decode']}")
+    out["bandwidth_guard"] = guard_legs(out, peaks["hbm_read_GBs"])
+    if out["bandwidth_guard"]["suspicious"]:
+        log(f"SUSPICIOUS (above the measured read stream): {out['bandwidth_guard']['suspicious']}")
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
         log(f"cpu: {out['cpu_baseline']}")

@@ -9,6 +9,11 @@ ref_vectors.npz   inputs and outputs of the reference's cpu/forward_cpu.c helper
                   oracle/Makefile).
 quant_golden.npz  (w16 -> q, s) vectors from tools/quantize.py:quantize_rows, imported from the
                   reference tree: numpy's own rounding and dtype path, which no closed form pins.
+gpq8_golden.json  what tools/quantize.py:main writes for a seeded synthetic model (a 'GPT2' v1 file
+                  plus the manifest tools/export_gpt2.py would write beside it), for the default
+                  scheme and for --fp16-keep head: the header and flags bytes, the file size, the
+                  streamed-bytes and parameter counts and sha256(body) from its sidecar, and the
+                  sha256 of the whole file.  Nothing else pins the 'GPQ8' v2 layout.
 
 Only data is written (no reference source).  The forward's weights are not stored; the test
 regenerates them with bare_metal_gpt2_amd.synth.make_body(seed=SEED_FWD, plain=False).
@@ -98,9 +103,84 @@ def quant_golden():
     np.savez_compressed(os.path.join(HERE, "quant_golden.npz"), **out)
 
 
+SEED_GPQ8 = 4242
+GPQ8_EXPORT_NAMES = ["wte", "wpe"] + [f"h{L}.{t}" for L in range(12) for t in (
+    "ln_1.g", "ln_1.b", "attn.c_attn.w", "attn.c_attn.b", "attn.c_proj.w", "attn.c_proj.b",
+    "ln_2.g", "ln_2.b", "mlp.c_fc.w", "mlp.c_fc.b", "mlp.c_proj.w", "mlp.c_proj.b")] + ["ln_f.g", "ln_f.b"]
+
+
+def gpq8_golden():
+    """Run the reference's tools/quantize.py main on a seeded synthetic 'GPT2' file (default scheme
+    and --fp16-keep head) and keep the facts of each output file (the body is regenerated by the
+    tests from SEED_GPQ8)."""
+    import importlib
+    import tempfile
+    synth = importlib.import_module("bare_metal_gpt2_amd.synth") if "bare_metal_gpt2_amd" in sys.modules else None
+    if synth is None:
+        __graft_entry__.load_package()
+        synth = importlib.import_module("bare_metal_gpt2_amd.synth")
+    with tempfile.TemporaryDirectory() as tmp:
+        _gpq8_golden(synth, tmp)
+
+
+def _gpq8_golden(synth, tmp):
+    import hashlib
+    import json
+    body = synth.make_body(seed=SEED_GPQ8, plain=False)
+    src = os.path.join(tmp, "synth_fp32.bin")
+    oracle.write_gpt2_file(src, body)
+    # the manifest tools/export_gpt2.py writes beside the file (export_gpt2.py:92-107): byte offsets
+    # of each tensor from the start of the file (64-byte header first)
+    tensors, off = [], 64
+    for (name, shape, _), ename in zip(synth.layout(), GPQ8_EXPORT_NAMES):
+        n = int(np.prod(shape))
+        tensors.append({"name": ename, "shape": list(shape), "offset": off, "bytes": 4 * n})
+        off += 4 * n
+    with open(src + ".json", "w") as f:
+        json.dump({"tensors": tensors}, f)
+    spec = importlib.util.spec_from_file_location("ref_quantize", REF_TOOLS)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    out = {"seed": SEED_GPQ8, "plain": False, "variants": {}}
+    for variant in ("none", "head"):
+        dst = os.path.join(tmp, f"q_{variant}.bin")
+        argv = sys.argv
+        sys.argv = ["quantize.py", "--in", src, "--out", dst, "--fp16-keep", variant]
+        try:
+            mod.main()
+        finally:
+            sys.argv = argv
+        side = json.load(open(dst + ".json"))
+        raw = open(dst, "rb").read()
+        n_t = int(np.frombuffer(raw[:64], np.int32)[7])
+        flags = np.frombuffer(raw[64:64 + 4 * n_t], np.int32)
+        out["variants"][variant] = {
+            "keep": [int(f == 0) for f in flags],
+            "prefix_hex": raw[:64 + 4 * n_t].hex(),
+            "file_bytes": side["file_bytes"],
+            "quantized_params": side["quantized_params"],
+            "kept_fp16_params": side["kept_fp16_params"],
+            "streamed_weight_bytes": side["streamed_weight_bytes"],
+            "sha256_body": side["sha256"],
+            "sha256_file": hashlib.sha256(raw).hexdigest(),
+        }
+        assert len(raw) == side["file_bytes"]
+        os.remove(dst)
+        os.remove(dst + ".json")
+    os.remove(src)
+    os.remove(src + ".json")
+    with open(os.path.join(HERE, "gpq8_golden.json"), "w") as f:
+        json.dump(out, f, indent=1)
+
+
 if __name__ == "__main__":
     if not oracle.ref_available():
         oracle.build()
-    ref_vectors()
-    quant_golden()
+    which = sys.argv[1:] or ["ref", "quant", "gpq8"]
+    if "ref" in which:
+        ref_vectors()
+    if "quant" in which:
+        quant_golden()
+    if "gpq8" in which:
+        gpq8_golden()
     print("wrote", os.listdir(HERE))

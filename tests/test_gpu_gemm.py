@@ -113,10 +113,9 @@ def test_head_gemm_tail_columns(pkg, L):
     A = oracle.fp16_view(oracle.layernorm(x, np.ones(K, np.float32), np.zeros(K, np.float32)))
     W = f16v(rng, (N, K), 0.02)
     got = gemm(pkg, L, A, W, None)
-    rows = np.r_[0:32, 240:272, 480:512]
-    tol_check(got[rows], oracle.matmul(A[rows], W))
+    tol_check(got, oracle.matmul(A, W))                      # every row and column
     tail = slice(50176, 50257)
-    tol_check(got[:, tail], oracle.matmul(A, W[tail]))
+    tol_check(got[:, tail], oracle.matmul(A, W[tail]))       # the 81 tail columns on their own
 
 
 @pytest.mark.parametrize("M,N,K", RAGGED)
@@ -264,7 +263,8 @@ def test_dispatch_rule(pkg, L):
 
 
 @pytest.mark.parametrize("kind", ["fp16", "int8"])
-@pytest.mark.parametrize("M,N,K", [(512, 768, 768), (512, 3072, 768), (200, 768, 3072), (33, 772, 768), (65, 770, 768)])
+@pytest.mark.parametrize("M,N,K", [(512, 768, 768), (512, 3072, 768), (200, 768, 3072), (33, 772, 768), (65, 770, 768),
+                                   (64, 768, 3072), (20, 770, 3072)])
 def test_fused_epilogues(pkg, L, kind, M, N, K):
     """The prefill's fused-epilogue GEMMs (forward_cuda.cu:99-105 folded into the GEMM: gelu_new of
     fp16(A.W^T + b), and fp16(resid + fp16(A.W^T + b)) with resid == C in place and in a separate

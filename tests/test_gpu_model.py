@@ -486,26 +486,137 @@ def test_persistent_decode_falls_back_without_gemv(pkg, L, synth, model):
 def test_persistent_decode_timeout_is_reported(pkg, L, synth, model):
     """Error path forced from the host: with a zero-round poll limit a work-group gives up at the
     first exchange word that has not arrived yet, every work-group still exits, and the sync call
-    reports the failure instead of returning a token."""
+    reports the failure instead of returning a token.  The same graph then recovers: with the default
+    limit restored, gpt2_decode_graph_set clears the error word and moves to a new epoch, so the words
+    the aborted step left behind cannot satisfy a poll, and the next step matches the eager step."""
     ids = synth.token_ids(8, seed=21)
     kv, scr, logits = decode_setup(pkg, L, model, ids, "gemv")
+    be = pkg.backend("gemv")
     tokens = pkg.Dev(1024 * 4)
     L.gpt2_tune_decode_spin(0)
     try:
-        g = L.gpt2_decode_graph_create_mode(pkg.backend("gemv"), C.byref(model.gpu), C.byref(kv.kv),
+        g = L.gpt2_decode_graph_create_mode(be, C.byref(model.gpu), C.byref(kv.kv),
                                             C.byref(scr.s), logits.ptr, tokens.ptr, pkg.DECODE_PERSISTENT)
+        assert g, pkg.check("graph create")
+        try:
+            assert L.gpt2_decode_graph_mode(g) == pkg.DECODE_PERSISTENT
+            tok, pos = C.c_int(), C.c_int()
+            assert L.gpt2_decode_graph_set(g, 5, len(ids)) == 0
+            assert L.gpt2_decode_graph_run(g, 1) == 0
+            assert L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)) != 0
+            assert L.gpt2_last_error() != 0
+            L.gpt2_tune_decode_spin(-1)
+            # the eager step at the same position, then the recovered persistent step
+            kv.kv.len = len(ids)
+            L.gpt2_decode_step_cuda(be, C.byref(model.gpu), C.byref(kv.kv), 5, len(ids), C.byref(scr.s),
+                                    logits.ptr, None)
+            pkg.check("eager step")
+            ref16 = logits.numpy(np.uint16, (V,)).copy()
+            assert L.gpt2_decode_graph_set(g, 5, len(ids)) == 0
+            assert L.gpt2_decode_graph_run(g, 1) == 0
+            assert L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)) == 0, pkg.check("recovered step")
+            assert pos.value == len(ids) + 1
+            lg = logits.numpy(np.uint16, (V,))
+            got, ref = oracle.f16_to_f32(lg)[None], oracle.f16_to_f32(ref16)[None]
+            assert rel_err(got, ref) <= 1e-2
+            assert kl_rows(ref, got).max() < 2e-3
+            assert tok.value == first_argmax(lg)
+        finally:
+            L.gpt2_decode_graph_destroy(g)
     finally:
         L.gpt2_tune_decode_spin(-1)
-    assert g, pkg.check("graph create")
-    try:
-        assert L.gpt2_decode_graph_mode(g) == pkg.DECODE_PERSISTENT
-        tok, pos = C.c_int(), C.c_int()
-        assert L.gpt2_decode_graph_set(g, 5, len(ids)) == 0
-        assert L.gpt2_decode_graph_run(g, 1) == 0
-        assert L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)) != 0
-        assert L.gpt2_last_error() != 0
-    finally:
-        L.gpt2_decode_graph_destroy(g)
     L.gpt2_last_error()
     scr.free()
     kv.free()
+
+
+# ------------------------------------------------------------------ config 5 at full scale
+@pytest.fixture(scope="module")
+def int8_ref_body(synth, body):
+    """The oracle's view of the INT8 model: every tensor as the fp16 engine holds it, and each trunk
+    matrix replaced by its dequantized weights fl32(q*s) (tools/dequant_check.py:61-65), not rounded
+    again; the tied head stays fp16 (the reference's default INT8 build)."""
+    out = oracle.fp16_view(body)
+    off = synth.offsets()
+    for Lyr in range(12):
+        for name in ("qkv_w", "attn_proj_w", "fc_w", "proj_w"):
+            o, shape = off[f"h{Lyr}.{name}"]
+            n = int(np.prod(shape))
+            q, s, _ = oracle.quantize_fp16_view(body[o:o + n].reshape(shape))
+            out[o:o + n] = oracle.dequantize(q, s).reshape(-1)
+    return out
+
+
+def test_config5_prefill_p512_vs_oracle(pkg, L, synth, model, int8_ref_body):
+    """BASELINE config 5's prefill at full size against the fp32 oracle, the reference's gate (a)/(c)
+    (bench/correctness_cuda.cu:200-219): P=512 random ids through the INT8 trunk (48 matrices, the
+    fused prefill) and the fp16 tied head, every layer's residual stream rel_err <= 1e-2, the final
+    LayerNorm and all 512 logits rows rel_err <= 1e-2, max KL < 0.02 over the rows."""
+    ids = synth.token_ids(512, seed=512)
+    model.quantize()
+    try:
+        got = gpu_forward(pkg, L, model, ids, "int8", logits_all=True, want_blocks=True)
+    finally:
+        L.gpt2_quant_free(C.byref(model.q))
+        model.q = None
+        model.gpu.q = None
+    ref = oracle.forward(int8_ref_body, ids, logits_all=True, want_blocks=True)
+    for Lyr in range(12):
+        assert rel_err(got["blocks"][Lyr], ref["blocks"][Lyr]) <= 1e-2, Lyr
+    assert rel_err(got["final_ln"], ref["final_ln"]) <= 1e-2
+    assert rel_err(got["logits"], ref["logits"]) <= 1e-2
+    assert kl_rows(ref["logits"], got["logits"]).max() < 0.02
+
+
+def test_config5_decode_512_steps_vs_oracle(pkg, L, synth, model, int8_ref_body):
+    """BASELINE config 5's decode at full depth, the reference's deepest cache gate
+    (bench/kv_gate.cu:15,190-219): from a 512-token INT8 prefill, 512 consecutive greedy steps of the
+    graph-replayed persistent step (positions 512..1023, the device state carrying token and
+    position from step to step), each step's logits against the matching row of ONE oracle forward
+    over the 1024 tokens the GPU consumed (prompt + its own greedy tokens).  Per position: rel_err
+    <= 1e-2 and KL < 0.02; the token each step picks is the first argmax of its own logits."""
+    P, n = 512, 512
+    ids = synth.token_ids(P, seed=5120)
+    model.quantize()
+    try:
+        kv, scr, logits = decode_setup(pkg, L, model, ids, "int8")
+        first_row = logits.numpy(np.uint16, (V,)).copy()
+        first = first_argmax(first_row)
+        tokens = pkg.Dev(1024 * 4)
+        g = L.gpt2_decode_graph_create_mode(pkg.backend("int8"), C.byref(model.gpu), C.byref(kv.kv),
+                                            C.byref(scr.s), logits.ptr, tokens.ptr, pkg.DECODE_PERSISTENT)
+        assert g, pkg.check("graph create")
+        rows, toks = [], []
+        try:
+            assert L.gpt2_decode_graph_mode(g) == pkg.DECODE_PERSISTENT
+            assert L.gpt2_decode_graph_set(g, first, P) == 0
+            tok, pos = C.c_int(), C.c_int()
+            for i in range(n):
+                assert L.gpt2_decode_graph_run(g, 1) == 0
+                assert L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)) == 0, pkg.check(f"step {i}")
+                assert pos.value == P + i + 1
+                lg = logits.numpy(np.uint16, (V,))
+                rows.append(lg)
+                assert tok.value == first_argmax(lg), i
+                toks.append(tok.value)
+        finally:
+            L.gpt2_decode_graph_destroy(g)
+        scr.free()
+        kv.free()
+    finally:
+        L.gpt2_quant_free(C.byref(model.q))
+        model.q = None
+        model.gpu.q = None
+    seq = np.concatenate([ids, [first], toks[:-1]]).astype(np.int32)
+    assert seq.size == P + n == 1024
+    ref = oracle.forward(int8_ref_body, seq, logits_all=True)["logits"]
+    got = oracle.f16_to_f32(np.stack(rows))
+    # step i ran at position P + i and predicts the token after seq[P + i]: oracle row P + i
+    refr = ref[P:P + n]
+    per_rel = [rel_err(got[i], refr[i]) for i in range(n)]
+    kl = kl_rows(refr, got)
+    worst = int(np.argmax(per_rel))
+    assert max(per_rel) <= 1e-2, (worst, per_rel[worst])
+    assert kl.max() < 0.02, (int(np.argmax(kl)), float(kl.max()))
+    # the prefill's last row against the oracle's row P-1
+    assert rel_err(oracle.f16_to_f32(first_row)[None], ref[P - 1:P]) <= 1e-2

@@ -131,3 +131,47 @@ def test_quant_file_round_trip(pkg, L, synth, tmp_path):
         L.gpt2_quant_free(C.byref(q2))
     finally:
         m.free()
+
+
+@pytest.mark.parametrize("variant", ["none", "head"])
+def test_gpq8_file_matches_reference_writer(pkg, L, synth, tmp_path, variant):
+    """The library's 'GPQ8' v2 writer and loader against the file tools/quantize.py:main wrote for the
+    same seeded model (tests/golden/gpq8_golden.json; default scheme and --fp16-keep head): the
+    device-quantized weights written by gpt2_quant_write_file give the same header and flags bytes,
+    the same file size, the same sha256 of the q/s body and of the whole file; gpt2_quant_load_upload
+    reads it back with the sidecar's streamed-byte count and the same codes and scales."""
+    import hashlib
+    import json
+    import os
+    gold = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "gpq8_golden.json")))
+    want = gold["variants"][variant]
+    body = synth.make_body(seed=gold["seed"], plain=gold["plain"])
+    m = pkg.Model(body)
+    path = str(tmp_path / f"w_{variant}.gpq8")
+    keep = (C.c_int * len(want["keep"]))(*want["keep"])
+    try:
+        m.quantize(want["keep"])
+        assert L.gpt2_quant_write_file(path.encode(), C.byref(m.q), keep) == 0
+        raw = open(path, "rb").read()
+        npre = len(want["prefix_hex"]) // 2
+        assert raw[:npre].hex() == want["prefix_hex"]
+        assert len(raw) == want["file_bytes"]
+        assert hashlib.sha256(raw[npre:]).hexdigest() == want["sha256_body"]
+        assert hashlib.sha256(raw).hexdigest() == want["sha256_file"]
+        q2 = pkg.GPT2QWeightsGPU()
+        assert L.gpt2_quant_load_upload(path.encode(), None, C.byref(q2)) == 0
+        try:
+            assert q2.streamed_bytes == want["streamed_weight_bytes"]
+            assert q2.nq == m.q.nq and q2.ns == m.q.ns
+            a, b = np.empty(m.q.nq, np.int8), np.empty(m.q.nq, np.int8)
+            L.gpt2_d2h(a.ctypes.data, m.q.qdata, a.nbytes)
+            L.gpt2_d2h(b.ctypes.data, q2.qdata, b.nbytes)
+            assert np.array_equal(a, b)
+            sa, sb = np.empty(m.q.ns, np.float32), np.empty(m.q.ns, np.float32)
+            L.gpt2_d2h(sa.ctypes.data, m.q.sdata, sa.nbytes)
+            L.gpt2_d2h(sb.ctypes.data, q2.sdata, sb.nbytes)
+            assert np.array_equal(sa.view(np.uint32), sb.view(np.uint32))
+        finally:
+            L.gpt2_quant_free(C.byref(q2))
+    finally:
+        m.free()

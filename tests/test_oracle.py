@@ -289,3 +289,52 @@ def test_quantize_fp16_view_and_dequant():
     deq = oracle.dequantize(q, s)
     assert np.array_equal(deq, (q.astype(np.float32) * s[:, None]).astype(np.float32))
     assert np.abs(deq - oracle.fp16_view(w32)).max() <= s.max() / 2 * 1.0001   # half a step at most
+
+
+# ------------------------------------------------- 'GPQ8' v2 layout (tools/quantize.py:153-172)
+GPQ8_TENSORS = ["wte"] + [f"h{L}.{t}" for L in range(12) for t in ("qkv_w", "attn_proj_w", "fc_w", "proj_w")]
+
+
+def gpq8_expected(synth, body, keep):
+    """Header + flags bytes, body sha256, file size and streamed bytes of the 'GPQ8' v2 file the
+    oracle's quantizer gives for `body`: the header dims, the int32 flags, then q and s per quantized
+    tensor in the order wte, 12 x {qkv, attn_proj, fc, proj} (tools/quantize.py:107-112,153-163)."""
+    import hashlib
+    hdr = np.zeros(16, np.int32)
+    hdr[:8] = [0x38515047, 2, 12, 768, 50257, 3072, 2304, len(GPQ8_TENSORS)]
+    flags = np.array([0 if k else 1 for k in keep], np.int32)
+    h = hashlib.sha256()
+    nbody = nq = ns = kept = 0
+    for name, k in zip(GPQ8_TENSORS, keep):
+        w = synth.tensor(body, name)
+        if k:
+            kept += w.size
+            continue
+        q, s, _ = oracle.quantize_fp16_view(w)
+        h.update(q.tobytes())
+        h.update(s.tobytes())
+        nbody += q.nbytes + s.nbytes
+        nq += q.size
+        ns += s.size
+    prefix = hdr.tobytes() + flags.tobytes()
+    return {"prefix_hex": prefix.hex(), "sha256_body": h.hexdigest(), "file_bytes": len(prefix) + nbody,
+            "streamed_weight_bytes": nq + 4 * ns + 2 * kept, "quantized_params": nq, "kept_fp16_params": kept}
+
+
+@pytest.mark.parametrize("variant", ["none", "head"])
+def test_gpq8_layout_matches_reference_writer(variant):
+    """The oracle's quantizer and the 'GPQ8' v2 layout against tests/golden/gpq8_golden.json, which
+    tools/quantize.py:main itself wrote for the same seeded model (default scheme, --fp16-keep head):
+    equal header and flags bytes, sha256 of the q/s body, file size and streamed-byte count."""
+    import importlib
+    import json
+    import __graft_entry__
+    __graft_entry__.load_package()
+    synth = importlib.import_module("bare_metal_gpt2_amd.synth")
+    gold = json.load(open(os.path.join(GOLD, "gpq8_golden.json")))
+    want = gold["variants"][variant]
+    body = synth.make_body(seed=gold["seed"], plain=gold["plain"])
+    got = gpq8_expected(synth, body, want["keep"])
+    for key in ("prefix_hex", "sha256_body", "file_bytes", "streamed_weight_bytes", "quantized_params",
+                "kept_fp16_params"):
+        assert got[key] == want[key], key
