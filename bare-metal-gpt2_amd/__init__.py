@@ -177,6 +177,7 @@ SIGNATURES = {
     "gpt2_tune_gemm_count": (_i, []),
     "gpt2_tune_gemm_name": (C.c_char_p, [_i]),
     "gpt2_tune_gemm_pick": (_i, [_i, _i, _i]),
+    "gpt2_tune_gemm_pick_q": (_i, [_i, _i, _i, _i]),
     "gpt2_tune_gemm_fits": (_i, [_i, _i]),
     "gpt2_tune_gemm_force": (None, [_i]),
     "gpt2_tune_gemm_run": (None, [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i]),

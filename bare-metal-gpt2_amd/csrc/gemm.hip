@@ -685,7 +685,7 @@ static const GemmCfg kCfgs[] = {
     G2_DCFGUF(48, 32, 3, 2, 8, 2, 4), // 33: as 15, four k-tiles per barrier (160 KB of LDS; INT8 mlp-proj)
     G2_DCFGUF(48, 64, 3, 2, 4, 1, 2),   // 34: 6 waves, wave tile 16x32 (each widened INT8 fragment feeds 2 MFMAs)
     G2_DCFGUF(48, 32, 3, 1, 4, 1, 2),   // 35: 3 waves, wave tile 16x32 (INT8 QKV, fc)
-    G2_DCFGU(48, 64, 3, 2, 4, 2, 2),    // 36: two k groups of 6 waves, wave tile 16x32
+    G2_DCFGUF(48, 64, 3, 2, 4, 2, 2),   // 36: two k groups of 6 waves, wave tile 16x32
     G2_DCFGU(96, 64, 3, 2, 4, 1, 2),    // 37: 6 waves, wave tile 32x32
     G2_DCFGUF(48, 32, 3, 1, 8, 2, 4),   // 38: two k groups of 3 waves, 8 stages, 4 k-tiles per barrier
     G2_DCFGUF(48, 32, 3, 1, 6, 2, 2),   // 39: two k groups of 3 waves, 6 stages
@@ -725,40 +725,45 @@ static int forced_cfg() {
     return g_force_cfg;
 }
 
+// Measured picks for the GPT-2 trunk shapes, by prompt length: each shape's 12 layer GEMMs
+// (distinct weights) back to back on MI355X, every config of the table timed per M bucket (fp16 and
+// INT8 weights), then for M in (256, 512] the whole step (12 layers x {QKV, attn-proj, fc, mlp-proj})
+// timed over per-shape candidates, because a kernel's best config alone and inside the step differ
+// (attn-proj most).  Buckets: M <= 64, <= 128, <= 256, <= 512, <= 1024; shapes QKV, attn-proj, fc,
+// mlp-proj; {fp16, INT8}.  Every config the prefill picks for attn-proj, fc and mlp-proj carries the
+// fused-epilogue kernels (gelu, residual).
+//   * short prompts take small tiles with k groups: 32x32 tiles with four k groups (47) keep 256+
+//     waves busy on mlp-proj's K=3072 (M=128: 6.6 us against 10.1 with one group) and on every INT8
+//     shape up to M=256 (M=64 QKV: 3.95 against 6.3 us), where each wave widens fewer W rows;
+//   * M in (256, 512] (the P=512 headline): 48-row W tiles, chosen inside the step;
+//   * M up to 1024: 96x64 / 128x128 tiles for fp16 QKV and fc (10.4 / 10.9 us), 64x64 for mlp-proj
+//     (12.9 against 16.5 us), 48x64 with two k groups (36) for attn-proj and the INT8 GEMMs.
+static const int kPick[5][4][2] = {
+    /* M <= 64   */ {{8, 47}, {8, 47}, {8, 47}, {47, 47}},
+    /* M <= 128  */ {{8, 39}, {8, 47}, {8, 39}, {47, 47}},
+    /* M <= 256  */ {{29, 36}, {8, 47}, {40, 36}, {47, 45}},
+    /* M <= 512  */ {{35, 35}, {25, 31}, {26, 35}, {23, 45}},
+    /* M <= 1024 */ {{0, 35}, {36, 36}, {6, 35}, {5, 36}},
+};
+
 static int pick_cfg(int M, int N, int K, bool qw = false) {
     if (forced_cfg() >= 0 && cfg_fits(g_force_cfg, K)) return g_force_cfg;
-    // Measured picks for the GPT-2 prefill shapes at M in (256, 512]: a grid over per-shape configs
-    // timed as the whole step (12 layers x {QKV, attn-proj, fc, mlp-proj}, distinct weights, back to
-    // back on MI355X; a kernel's best config alone and inside the step differ, attn-proj most),
-    // then a fallback: the largest tile that still
-    // gives about one work-group per CU (256 CUs), among the configs whose K constraint holds; -1
-    // when none does (the guarded kernel runs).
-    if (M > 256 && M <= 512 && qw) {
-        // INT8 weights (widened to fp16 as fragments are read), picked the same way on an INT8 step:
-        // QKV and fc take 16x32 wave tiles (3 waves), so each widened W fragment feeds two MFMAs and
-        // fewer waves widen the same rows (400.5 us per step, against 425.4 with the fp16 picks'
-        // shapes and 467.3 with the fp16 table itself); mlp-proj (K=3072) splits K over four groups
-        // of such waves (367.6 against 381.2 us with two groups of 6 waves).
-        int c = -1;
-        if (N == 2304 && K == 768) c = 35;                // QKV: 48x32, 3 waves, 2 k-tiles/barrier
-        else if (N == 768 && K == 768) c = 31;            // attn-proj: 48x32, 8 stages, 4/barrier
-        else if (N == 3072 && K == 768) c = 35;           // fc: as QKV
-        else if (N == 768 && K == 3072) c = 45;           // mlp-proj: 48x32, 4 k groups of 3 waves, 2/barrier
-        if (c >= 0 && cfg_fits(c, K)) return c;
+    int shape = -1;
+    if (N == 2304 && K == 768) shape = 0;            // QKV
+    else if (N == 768 && K == 768) shape = 1;        // attn-proj
+    else if (N == 3072 && K == 768) shape = 2;       // fc
+    else if (N == 768 && K == 3072) shape = 3;       // mlp-proj
+    if (shape >= 0 && M >= 2 && M <= 1024) {
+        const int bucket = M <= 64 ? 0 : M <= 128 ? 1 : M <= 256 ? 2 : M <= 512 ? 3 : 4;
+        const int c = kPick[bucket][shape][qw ? 1 : 0];
+        if (cfg_fits(c, K)) return c;
     }
-    if (M > 256 && M <= 512) {
-        int c = -1;
-        if (N == 768 && K == 768) c = 25;                 // attn-proj: 48x32, 6 waves, 6 stages, 2/barrier
-        else if (N == 768 && K == 3072) c = 23;           // mlp-proj: 48x32, 2 k groups, 6 stages, 2/barrier
-        else if (N == 2304 && K == 768) c = 35;           // QKV: 48x32, 3 waves (16x32 wave tiles), 2 k-tiles/barrier
-        else if (N == 3072 && K == 768) c = 26;           // fc: 48x64, 12 waves, 2 k-tiles/barrier
-        if (c >= 0 && cfg_fits(c, K)) return c;
-    }
-    // Vocabulary-sized N (the tied head, 50257 rows of W): many tiles per CU, where large tiles win
-    // on L2 bytes per FLOP (M=512: 128x64 83 us, 256x128 88, 128x128 94, 48-row tiles >= 135) and
-    // the 128x64 tile double-buffered (three work-groups per CU) beats its 3-stage form (64 vs 74 us).
-    // Few rows and a long K (mlp-proj of a 64-token prefill: 24 x 2 tiles of 32x32): four k groups per
-    // tile keep more waves busy (M=64: 6.9 us against 9+ us with one group).
+    // Other shapes: vocabulary-sized N (the tied head, 50257 rows of W) has many tiles per CU, where
+    // large tiles win on L2 bytes per FLOP (M=512: 128x64 83 us, 256x128 88, 128x128 94, 48-row
+    // tiles >= 135) and the 128x64 tile double-buffered (three work-groups per CU) beats its 3-stage
+    // form (64 vs 74 us).  Few rows and a long K: four k groups per tile keep more waves busy.
+    // Otherwise the largest tile that still gives about one work-group per CU (256 CUs), among the
+    // configs whose K constraint holds; -1 when none does (the guarded kernel runs).
     if (M <= 64 && K >= 2048 && N <= 4096 && cfg_fits(47, K)) return 47;
     if (N >= 16384 && M > 32 && cfg_fits(46, K)) return 46;
     if (N >= 16384 && M > 32 && cfg_fits(1, K)) return 1;
@@ -865,6 +870,7 @@ extern "C" void gpt2_matmul_naive(gpt2_half *C, const gpt2_half *A, const gpt2_h
 extern "C" int gpt2_tune_gemm_count(void) { return kNumCfgs; }
 extern "C" const char *gpt2_tune_gemm_name(int cfg) { return cfg >= 0 && cfg < kNumCfgs ? kCfgs[cfg].name : "?"; }
 extern "C" int gpt2_tune_gemm_pick(int M, int N, int K) { return pick_cfg(M, N, K); }
+extern "C" int gpt2_tune_gemm_pick_q(int M, int N, int K, int int8) { return pick_cfg(M, N, K, int8 != 0); }
 extern "C" int gpt2_tune_gemm_fits(int cfg, int K) { return cfg >= 0 && cfg < kNumCfgs && cfg_fits(cfg, K); }
 // Force one config for every later GEMM whose K it accepts (-1 restores the table).
 extern "C" void gpt2_tune_gemm_force(int cfg) { g_force_cfg = (cfg >= 0 && cfg < kNumCfgs) ? cfg : -1; }

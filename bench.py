@@ -17,6 +17,10 @@ Also reported in the same JSON line:
   head_gemv     fp16 tied-head GEMV (77.3 MB) cold / warm
   gemm_int8_set the same P=512 trunk set with INT8 weights (the config-5 prefill GEMMs)
   head_gemm     the tied head as a prefill GEMM, [512x768] . [768x50257]^T (39.5 GFLOP)
+  gemm_m_sweep  the four trunk GEMMs at M in {1, 64, 128, 256, 512, 1024}, fp16 and INT8 weights
+  measured_peaks  this box's HBM read stream and fp16 MFMA issue rate, beside the datasheet peaks
+  bandwidth_guard  every cold (HBM) GB/s leg against the measured read stream (the reference's bug
+                line): legs above it are listed as suspicious
   attention_prefill  causal MFMA prefill attention per launch at T=512 and T=1024 (12 heads x 64)
   forward_t64   config 1 on the GPU: the fp16 forward at T=64 with logits for all 64 rows
   decode        GPT-2-124M decode tok/s @ctx=512: INT8 trunk + fp16 head, one hipGraph replay per
@@ -308,6 +312,40 @@ def bench_gemm_extra(B, steps):
     return int8, head
 
 
+# ------------------------------------------------------------------------------ M sweep
+def bench_m_sweep(B, Ms=(1, 64, 128, 256, 512, 1024), iters=30):
+    """The four trunk GEMMs across prompt lengths (the reference's bench/profile_matmul.cu:6-16 sweep):
+    per shape, 12 layers' distinct weights back to back through gpt2_matmul_tiled / gpt2_matmul_int8,
+    per-launch microseconds and TFLOP/s (M = 1 runs the GEMV path, as the launchers route it)."""
+    rng = np.random.default_rng(555)
+    L = B.L
+    out = {}
+    for kind in ("fp16", "int8"):
+        rows = []
+        for name, N, K in GEMM_SET:
+            if kind == "int8":
+                Ws = [B.dev(rng.integers(-127, 128, (N, K), dtype=np.int8)) for _ in range(N_LAYER)]
+                sc = B.dev(np.full(N, 1e-3, np.float32))
+            else:
+                Ws = [B.dev(f16(rng, (N, K), 0.02)) for _ in range(N_LAYER)]
+                sc = None
+            b = B.dev(f16(rng, N, 0.01))
+            for M in Ms:
+                A = B.dev(f16(rng, (M, K), 1.0))
+                Cm = B.empty(M * N * 2)
+                ops = [B.op(1 if kind == "int8" else 0, Cm.ptr, A.ptr, w.ptr, sc.ptr if sc else None, b.ptr, M, N, K)
+                       for w in Ws]
+                ms, _ = B.run_ops(ops, 3, iters)
+                us = ms * 1e3 / N_LAYER
+                cfg = L.gpt2_tune_gemm_pick_q(M, N, K, 1 if kind == "int8" else 0)
+                rows.append({"gemm": name, "M": M, "us": round(us, 3),
+                             "tflops": round(2.0 * M * N * K / (us * 1e-6) / 1e12, 2),
+                             "kernel": "gemv" if M == 1 else L.gpt2_tune_gemm_name(cfg).decode()})
+            B.keep.clear()
+        out[kind] = rows
+    return out
+
+
 # ------------------------------------------------------------------------------ prefill attention
 def bench_attention(B):
     """Causal prefill attention (gpt2_attention_flash) over qkv[T, 2304], 12 heads x 64 dims.  FLOPs
@@ -510,8 +548,9 @@ def bench_decode(B, steady_reps=64):
 def measured_peaks(B, cus):
     """This box's ceilings, measured in the same run beside the datasheet peaks (the role of
     bench/microbench.cu:69-377 in the reference): the HBM read stream over 4 GiB (16x the 256 MB
-    MALL, so every byte comes from HBM) and the fp16 MFMA issue loop (v_mfma_f32_16x16x32_f16, eight
-    independent accumulators per wave, one work-group of four waves per CU)."""
+    MALL, so every byte comes from HBM; the faster of two launch shapes) and the fp16 MFMA issue loop
+    (v_mfma_f32_32x32x16_f16, four independent accumulators per wave, one work-group of four waves
+    per CU)."""
     L = B.L
     nbytes = 4 << 30
     buf = B.pkg.Dev(nbytes)
@@ -521,13 +560,14 @@ def measured_peaks(B, cus):
         B.pkg.check("gpt2_bench_read")
     read_gbs = nbytes / (ms.value * 1e-3) / 1e9
     buf.free()
-    blocks, iters = 4 * cus, 20000
+    blocks, iters = cus, 20000
     if L.gpt2_bench_mfma(blocks, iters, C.byref(ms)):
         B.pkg.check("gpt2_bench_mfma")
-    mfma_tflops = blocks * 4.0 * iters * 8 * (16 * 16 * 32 * 2) / (ms.value * 1e-3) / 1e12
+    mfma_tflops = blocks * 4.0 * iters * 4 * (32 * 32 * 16 * 2) / (ms.value * 1e-3) / 1e12
     return {"hbm_read_GBs": round(read_gbs, 1), "hbm_read_bytes": nbytes,
-            "mfma_fp16_tflops": round(mfma_tflops, 1), "mfma_loop": f"{blocks} work-groups x 4 waves x {iters} x 8 "
-            "v_mfma_f32_16x16x32_f16", "datasheet": {"hbm_GBs": PEAK_HBM_GBS, "mfma_fp16_tflops": PEAK_FP16_TFLOPS}}
+            "mfma_fp16_tflops": round(mfma_tflops, 1), "mfma_loop": f"{blocks} work-groups x 4 waves x {iters} x 4 "
+            "v_mfma_f32_32x32x16_f16 (one wave per SIMD; the clock drops to ~1.7 GHz under this load)",
+            "datasheet": {"hbm_GBs": PEAK_HBM_GBS, "mfma_fp16_tflops": PEAK_FP16_TFLOPS}}
 
 
 def guard_legs(out, read_gbs):
@@ -721,6 +761,9 @@ def main():
         out["head_gemv_fp16"] = head
         out["gemm_int8_set"], out["head_gemm_fp16"] = bench_gemm_extra(B, args.steps)
         log(f"int8 gemm set: {out['gemm_int8_set']}\nhead gemm: {out['head_gemm_fp16']}")
+        out["gemm_m_sweep"] = bench_m_sweep(B)
+        B.keep.clear()
+        log(f"m sweep: {out['gemm_m_sweep']}")
         out["attention_prefill"] = bench_attention(B)
         B.keep.clear()
         log(f"attention: {out['attention_prefill']}")

@@ -227,3 +227,17 @@ def test_quant_file_errors(L, pkg, tmp_path, case):
 def test_error_strings(L):
     assert L.gpt2_error_string(0) == b"no error"
     assert b"invalid argument" in L.gpt2_error_string(1000)
+
+
+def test_c_caller_builds_and_links():
+    """tests/c/boundary_caller.c compiles as C11 against include/ alone (gcc -Wall -Werror, done by
+    __graft_entry__.build()), links libgpt2amd.so, and with no arguments prints its usage and exits 2
+    before any device call."""
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    exe = os.path.join(root, "tests", "c", "boundary_caller")
+    assert os.path.exists(exe)
+    deps = subprocess.run(["ldd", exe], capture_output=True, text=True).stdout
+    assert "libgpt2amd.so" in deps and "not found" not in deps.split("libgpt2amd.so", 1)[1].splitlines()[0]
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2 and "usage" in r.stderr

@@ -77,6 +77,26 @@ def test_int8_config_shapes(pkg, L, M, N, K):
     tol_check(got, oracle.matmul(A, oracle.dequantize(q, s), b))
 
 
+TRUNK_NK = [(2304, 768), (768, 768), (3072, 768), (768, 3072)]
+
+
+@pytest.mark.parametrize("kind", ["fp16", "int8"])
+@pytest.mark.parametrize("M", [2, 64, 100, 128, 200, 256, 700, 1024])
+def test_trunk_shapes_every_m_bucket(pkg, L, kind, M):
+    """The four trunk shapes at prompt lengths in every bucket of the tile table (M <= 64, 128, 256,
+    512, 1024), including the longest prefill (M = 1024) and ragged M, against the oracle."""
+    for N, K in TRUNK_NK:
+        rng = np.random.default_rng(M * 5 + N + K)
+        A, b = f16v(rng, (M, K), 1.0), f16v(rng, N, 0.01)
+        if kind == "int8":
+            q, s, _ = oracle.quantize_fp16_view(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+            got = gemm(pkg, L, A, None, b, kind="int8", q=q, s=s)
+            tol_check(got, oracle.matmul(A, oracle.dequantize(q, s), b))
+        else:
+            W = f16v(rng, (N, K), 0.02)
+            tol_check(gemm(pkg, L, A, W, b), oracle.matmul(A, W, b))
+
+
 @pytest.mark.parametrize("kind", ["fp16", "int8"])
 @pytest.mark.parametrize("M,N,K", [(300, 777, 768), (129, 257, 256), (64, 1001, 192), (512, 2305, 768)])
 def test_unaligned_c_rows(pkg, L, kind, M, N, K):
@@ -264,7 +284,8 @@ def test_dispatch_rule(pkg, L):
 
 @pytest.mark.parametrize("kind", ["fp16", "int8"])
 @pytest.mark.parametrize("M,N,K", [(512, 768, 768), (512, 3072, 768), (200, 768, 3072), (33, 772, 768), (65, 770, 768),
-                                   (64, 768, 3072), (20, 770, 3072)])
+                                   (64, 768, 3072), (20, 770, 3072), (128, 3072, 768), (128, 768, 3072),
+                                   (1024, 768, 768), (1024, 3072, 768), (1000, 768, 3072), (256, 3072, 768)])
 def test_fused_epilogues(pkg, L, kind, M, N, K):
     """The prefill's fused-epilogue GEMMs (forward_cuda.cu:99-105 folded into the GEMM: gelu_new of
     fp16(A.W^T + b), and fp16(resid + fp16(A.W^T + b)) with resid == C in place and in a separate
