@@ -124,6 +124,7 @@ SIGNATURES = {
     "gpt2_quant_write_file": (_i, [C.c_char_p, C.POINTER(GPT2QWeightsGPU), _vp]),
     "gpt2_forward_cuda": (None, [_BE, C.POINTER(GPT2WeightsGPU), _vp, _i, C.POINTER(GPT2ScratchGPU),
                                  C.POINTER(GPT2CapsGPU)]),
+    "gpt2_forward_noalloc": (None, [_BE, C.POINTER(GPT2WeightsGPU), _vp, _i, C.POINTER(GPT2CapsGPU)]),
     "gpt2_set_stream": (None, [_vp]),
     "gpt2_get_stream": (_vp, []),
     "gpt2_last_error": (_i, []),

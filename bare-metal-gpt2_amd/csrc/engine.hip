@@ -6,6 +6,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "common.h"
@@ -278,6 +279,59 @@ extern "C" void gpt2_forward_cuda(const GPT2Backend *be, const GPT2WeightsGPU *w
         if (caps->logits_all) gpt2_matmul_dispatch(be, caps->logits, s->ln, w->wte, qh, nullptr, T, V, E);
         else gpt2_matmul_dispatch(be, caps->logits, s->ln + (size_t)(T - 1) * E, w->wte, qh, nullptr, 1, V, E);
     }
+}
+
+// ============================================================================ forward, no allocation
+// gpt2_forward_cuda for callers that cannot allocate device memory (code under HIP graph capture,
+// serving loops, harnesses that forbid hipMalloc): the activations live in one file-scope device
+// array instead of a GPT2ScratchGPU.  Each GPU that runs it holds its own copy of the array until
+// the process ends; every call on a GPU reuses that GPU's copy, so calls that overlap on one GPU
+// (two host threads, two streams) race.  Nothing in the array needs clearing: every buffer is
+// written before it is read within a call.
+constexpr size_t NOALLOC_ROW = 5 * GPT2_N_EMBD + GPT2_QKV_DIM + GPT2_FFN_DIM;   // halves per token
+static __device__ __align__(256) uint16_t scratch[(size_t)GPT2_NOALLOC_MAX_T * NOALLOC_ROW];
+
+// The device address of `scratch` on the current device, looked up once per device.  (In host code
+// the array's name is a host-side stand-in, not a device address.)
+static std::mutex g_scratch_mu;
+static uint16_t *g_scratch_ptr[64];
+
+static uint16_t *scratch_ptr() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+        g_scratch_ptr[dev] = static_cast<uint16_t *>(p);
+    }
+    return g_scratch_ptr[dev];
+}
+
+extern "C" void gpt2_forward_noalloc(const GPT2Backend *be, const GPT2WeightsGPU *w, const int *d_ids, int T,
+                                     GPT2CapsGPU *caps) {
+    if (T > GPT2_NOALLOC_MAX_T) {
+        set_error(E_CAPACITY, "gpt2_forward_noalloc: T exceeds GPT2_NOALLOC_MAX_T (128 tokens of static scratch)");
+        return;
+    }
+    uint16_t *base = scratch_ptr();
+    if (!base) {
+        set_error(E_STATE, "gpt2_forward_noalloc: no device address for the static scratch");
+        return;
+    }
+    // the GPT2ScratchGPU buffers carved from the array, rows of T tokens (16-byte aligned: every width
+    // is a multiple of 8 halves)
+    const size_t t = (size_t)(T > 0 ? T : 0), E = GPT2_N_EMBD;
+    GPT2ScratchGPU s;
+    s.x = base;
+    s.ln = s.x + t * E;
+    s.qkv = s.ln + t * E;
+    s.att = s.qkv + t * GPT2_QKV_DIM;
+    s.ao = s.att + t * E;
+    s.fc = s.ao + t * E;
+    s.ff = s.fc + t * GPT2_FFN_DIM;
+    s.maxT = GPT2_NOALLOC_MAX_T;
+    gpt2_forward_cuda(be, w, d_ids, T, &s, caps);
 }
 
 // ============================================================================ KV cache

@@ -190,6 +190,15 @@ int gpt2_quant_write_file(const char *path, const GPT2QWeightsGPU *q, const int 
 /* cuda/kernels.cuh:116-117, forward_cuda.cu:77-116 */
 void gpt2_forward_cuda(const GPT2Backend *be, const GPT2WeightsGPU *w, const int *d_ids, int T,
                        GPT2ScratchGPU *s, GPT2CapsGPU *caps);
+/* No counterpart in the reference.  gpt2_forward_cuda without the scratch argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc): it calls no allocator; the activations live in a static device array of
+ * GPT2_NOALLOC_MAX_T tokens (2.25 MiB) that each GPU holds until the process ends.  T above the
+ * limit records E_CAPACITY (gpt2_last_error) and launches nothing.  Every call on one GPU shares that
+ * GPU's array, so calls that overlap on one GPU race. */
+#define GPT2_NOALLOC_MAX_T 128
+void gpt2_forward_noalloc(const GPT2Backend *be, const GPT2WeightsGPU *w, const int *d_ids, int T,
+                          GPT2CapsGPU *caps);
 
 /* ---- runtime: stream, errors, device memory (the cuda/common.cuh:17-66 helpers) ---------- */
 /* Stream used by every launcher from now on (a hipStream_t; NULL = the null stream). */
