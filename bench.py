@@ -193,8 +193,10 @@ def copies_for(nbytes, floor=600e6):
     return max(4, int(np.ceil(floor / nbytes)))
 
 
-def bench_gemv(B):
+def bench_gemv(B, quick=False):
+    """quick: a few launches per leg (the counter runs profile every dispatch)."""
     rng = np.random.default_rng(4321)
+    n_cold, n_warm, n_chain, n_head = (1, 20, 2, 10) if quick else (5, 2000, 200, 200)
     L = B.L
     res = {}
     x768 = B.dev(f16(rng, 768, 1.0))
@@ -213,13 +215,14 @@ def bench_gemv(B):
             L.gpt2_d2d(big.at(r * N * K), q.ptr, N * K)
         L.gpt2_sync()
         cold_ops = [B.op(3, y.ptr, x.ptr, big.at(r * N * K), s.ptr, b.ptr, 1, N, K) for r in range(R)]
-        ms_cold, _ = B.run_ops(cold_ops, 1, 5)
+        ms_cold, _ = B.run_ops(cold_ops, 1, n_cold)
         ms_cold /= R
-        ms_warm, _ = B.run_ops([B.op(3, y.ptr, x.ptr, q.ptr, s.ptr, b.ptr, 1, N, K)], 50, 2000)
+        ms_warm, _ = B.run_ops([B.op(3, y.ptr, x.ptr, q.ptr, s.ptr, b.ptr, 1, N, K)], 5 if quick else 50, n_warm)
         res[name] = {"N": N, "K": K, "bytes": algo, "copies": R,
                      "cold_us": round(ms_cold * 1e3, 3), "cold_GBs": round(algo / (ms_cold * 1e-3) / 1e9, 1),
                      "warm_us": round(ms_warm * 1e3, 3), "warm_GBs": round(algo / (ms_warm * 1e-3) / 1e9, 1)}
         big.free()
+        log(f"gemv {name}: {res[name]}")
     # the 48 INT8 GEMVs of one decode step, distinct weights per layer, back to back
     chain_bytes = 0
     for layer in range(N_LAYER):
@@ -230,7 +233,7 @@ def bench_gemv(B):
             b = B.dev(f16(rng, N, 0.01))
             chain.append(B.op(3, y.ptr, x.ptr, q.ptr, s.ptr, b.ptr, 1, N, K))
             chain_bytes += N * K + 4 * N + 2 * K + 4 * N
-    ms_chain, _ = B.run_ops(chain, 20, 200)
+    ms_chain, _ = B.run_ops(chain, 2 if quick else 20, n_chain)
     res["trunk_chain_48"] = {"bytes": chain_bytes, "us": round(ms_chain * 1e3, 2),
                              "GBs": round(chain_bytes / (ms_chain * 1e-3) / 1e9, 1)}
     # the same kernel on the INT8 tied head (38.6 MB, no bias): large enough that the launch floor
@@ -245,9 +248,10 @@ def bench_gemv(B):
     for r in range(R):
         L.gpt2_d2d(big.at(r * N * K), q.ptr, N * K)
     L.gpt2_sync()
-    ms_cold, _ = B.run_ops([B.op(3, y.ptr, x768.ptr, big.at(r * N * K), s.ptr, None, 1, N, K) for r in range(R)], 1, 5)
+    log(f"gemv chain: {res['trunk_chain_48']}")
+    ms_cold, _ = B.run_ops([B.op(3, y.ptr, x768.ptr, big.at(r * N * K), s.ptr, None, 1, N, K) for r in range(R)], 1, n_cold)
     ms_cold /= R
-    ms_warm, _ = B.run_ops([B.op(3, y.ptr, x768.ptr, q.ptr, s.ptr, None, 1, N, K)], 10, 200)
+    ms_warm, _ = B.run_ops([B.op(3, y.ptr, x768.ptr, q.ptr, s.ptr, None, 1, N, K)], 2 if quick else 10, n_head)
     res["head"] = {"N": N, "K": K, "bytes": algo, "copies": R,
                    "cold_us": round(ms_cold * 1e3, 3), "cold_GBs": round(algo / (ms_cold * 1e-3) / 1e9, 1),
                    "cold_frac_of_8TBs": round(algo / (ms_cold * 1e-3) / 8e12, 3),
@@ -262,9 +266,11 @@ def bench_gemv(B):
     head = f16(rng, (N, K), 0.02)
     for r in range(R):
         L.gpt2_h2d(big.at(r * N * K * 2), head.ctypes.data, head.nbytes)
-    ms_cold, _ = B.run_ops([B.op(2, y.ptr, x768.ptr, big.at(r * N * K * 2), None, None, 1, N, K) for r in range(R)], 1, 10)
+    log(f"gemv int8 head: {res['head']}")
+    ms_cold, _ = B.run_ops([B.op(2, y.ptr, x768.ptr, big.at(r * N * K * 2), None, None, 1, N, K) for r in range(R)], 1,
+                           2 * n_cold)
     ms_cold /= R
-    ms_warm, _ = B.run_ops([B.op(2, y.ptr, x768.ptr, big.ptr, None, None, 1, N, K)], 10, 200)
+    ms_warm, _ = B.run_ops([B.op(2, y.ptr, x768.ptr, big.ptr, None, None, 1, N, K)], 2 if quick else 10, n_head)
     head_res = {"N": N, "K": K, "bytes": algo, "copies": R, "cold_us": round(ms_cold * 1e3, 2),
                 "cold_GBs": round(algo / (ms_cold * 1e-3) / 1e9, 1), "warm_us": round(ms_warm * 1e3, 2),
                 "warm_GBs": round(algo / (ms_warm * 1e-3) / 1e9, 1)}
@@ -704,6 +710,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="only the headline GEMM set")
     ap.add_argument("--no-decode", action="store_true", help="skip the graph-replayed decode leg")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only the decode GEMV legs (INT8 trunk cold/warm, the 48-GEMV chain, INT8 and fp16 head) "
+                         "with a few launches each, printed as one JSON line: the driver for their rocprofv3 "
+                         "counter runs")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="also run one plain copy of BYTES (calibrates FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -733,6 +743,10 @@ def main():
         log(f"copy probe: {args.copy_probe} B in {ms.value * 1e3:.1f} us")
         src.free()
         dst.free()
+    if args.gemv_only:
+        gemv, head = bench_gemv(B, quick=True)
+        print(json.dumps({"gemv_int8": gemv, "head_gemv_fp16": head}), flush=True)
+        return
     flops_step, ms_step, shapes, roofline, ms_graph = bench_gemm_set(B, args.steps, args.warmup)
     value = flops_step / (ms_step * 1e-3) / 1e12
     log(f"prefill GEMM set: {ms_step * 1e3:.1f} us/step -> {value:.1f} TFLOP/s; per shape {shapes}")
