@@ -178,6 +178,9 @@ SIGNATURES = {
     "gpt2_tune_gemm_count": (_i, []),
     "gpt2_tune_gemm_name": (C.c_char_p, [_i]),
     "gpt2_tune_gemm_pick": (_i, [_i, _i, _i]),
+    "gpt2_tune_prefill_persistent": (None, [_i]),
+    "gpt2_tune_prefill_spin": (None, [_i]),
+    "gpt2_prefill_status": (_i, []),
     "gpt2_tune_gemm_pick_q": (_i, [_i, _i, _i, _i]),
     "gpt2_tune_gemm_fits": (_i, [_i, _i]),
     "gpt2_tune_gemm_force": (None, [_i]),

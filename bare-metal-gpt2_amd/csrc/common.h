@@ -147,6 +147,23 @@ __device__ __forceinline__ void i8x4_to_f16x4_v(uint32_t w, f16x2 &lo, f16x2 &hi
     hi = __builtin_bit_cast(f16x2, b) + off;
 }
 
+// The same widening as two f16x2 words (lo, hi) of 32 bits.
+__device__ __forceinline__ void i8x4_to_f16x4(uint32_t w, uint32_t &lo, uint32_t &hi) {
+    f16x2 a, b;
+    i8x4_to_f16x4_v(w, a, b);
+    lo = __builtin_bit_cast(uint32_t, a);
+    hi = __builtin_bit_cast(uint32_t, b);
+}
+
+// Eight int8 codes (two packed words) widened to eight exact fp16 values.
+__device__ __forceinline__ f16x8 i8x8_to_f16x8(uint2 w) {
+    uint32_t h[4];
+    i8x4_to_f16x4(w.x, h[0], h[1]);
+    i8x4_to_f16x4(w.y, h[2], h[3]);
+    const i32x4 v = {(int)h[0], (int)h[1], (int)h[2], (int)h[3]};
+    return __builtin_bit_cast(f16x8, v);
+}
+
 // Work-group barrier for LDS traffic: waits for this wave's LDS (and scalar) operations only, not for
 // its outstanding global loads and stores, which __syncthreads() also drains.  Loads issued ahead
 // (the next tile, the next phase's weights) stay in flight across it; the caller waits for those
@@ -160,6 +177,16 @@ template <int n>
 __device__ __forceinline__ void wait_vm() {
     static_assert(n >= 0 && n < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
+}
+
+// Wait until at most `after` k-tiles of this wave's loads (L instructions each) are outstanding
+// (after is a run-time value in [0, MAXA]; each case is an immediate s_waitcnt).
+template <int L, int MAXA>
+__device__ __forceinline__ void wait_tiles(int after) {
+    if constexpr (MAXA >= 0) {
+        if (after == MAXA) { wait_vm<L * MAXA>(); return; }
+        wait_tiles<L, MAXA - 1>(after);
+    }
 }
 
 }  // namespace g2

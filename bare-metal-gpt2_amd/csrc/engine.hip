@@ -11,6 +11,7 @@
 
 #include "common.h"
 #include "decode.h"
+#include "prefill.h"
 
 namespace g2 {
 void gemv(uint16_t *C, const uint16_t *x, const void *W, const float *Ws, const uint16_t *bias, int N, int K, bool qw,
@@ -237,8 +238,18 @@ static void matmul_site(const GPT2Backend *be, bool fused, gpt2_half *C, const g
     }
 }
 
+// persistent: the trunk may run as the persistent kernel (it allocates its arena on first use, so
+// the no-allocation entry point runs the launch sequence instead).
+static void forward_impl(const GPT2Backend *be, const GPT2WeightsGPU *w, const int *d_ids, int T, GPT2ScratchGPU *s,
+                         GPT2CapsGPU *caps, bool persistent);
+
 extern "C" void gpt2_forward_cuda(const GPT2Backend *be, const GPT2WeightsGPU *w, const int *d_ids, int T,
                                   GPT2ScratchGPU *s, GPT2CapsGPU *caps) {
+    forward_impl(be, w, d_ids, T, s, caps, true);
+}
+
+static void forward_impl(const GPT2Backend *be, const GPT2WeightsGPU *w, const int *d_ids, int T, GPT2ScratchGPU *s,
+                         GPT2CapsGPU *caps, bool persistent) {
     if (!be || !w || !w->data || !s || !d_ids || T <= 0 || T > s->maxT || T > GPT2_N_CTX) {
         arg_fail("gpt2_forward_cuda: bad arguments (T must be in [1, min(maxT, 1024)])");
         return;
@@ -249,6 +260,26 @@ extern "C" void gpt2_forward_cuda(const GPT2Backend *be, const GPT2WeightsGPU *w
     if (kv && T > kv->maxT) { arg_fail("gpt2_forward_cuda: T exceeds the KV cache"); return; }
 
     const bool fused = fused_prefill_ok(be);
+    // The 12-layer trunk as one persistent kernel (prefill.hip; switched off, so prefill_persist
+    // returns nullptr and the launch sequence below runs); the final LayerNorm, the head and the
+    // captures follow as launches.
+    if (fused && persistent) {
+        const uint16_t *x0 = nullptr, *xl[GPT2_N_LAYER];
+        const uint16_t *xf = prefill_persist(be, w, d_ids, T, kv, &x0, xl);
+        if (xf) {
+            if (caps && caps->embed) capcpy(caps->embed, x0, (size_t)T * E);
+            if (caps && caps->blocks)
+                for (int L = 0; L < GPT2_N_LAYER; ++L) capcpy(caps->blocks + (size_t)L * T * E, xl[L], (size_t)T * E);
+            be->layernorm(s->ln, xf, w->lnf_g, w->lnf_b, T, E);
+            if (caps && caps->final_ln) capcpy(caps->final_ln, s->ln, (size_t)T * E);
+            if (caps && caps->logits) {
+                const GPT2QW *qh = qw ? &qw->wte : nullptr;
+                if (caps->logits_all) gpt2_matmul_dispatch(be, caps->logits, s->ln, w->wte, qh, nullptr, T, V, E);
+                else gpt2_matmul_dispatch(be, caps->logits, s->ln + (size_t)(T - 1) * E, w->wte, qh, nullptr, 1, V, E);
+            }
+            return;
+        }
+    }
     // the attention launch fills the cache itself when it is this library's prefill attention
     const bool attn_kv = fused && be->attention == gpt2_attention_flash && kv && kv->data;
     be->embed(s->x, w->wte, w->wpe, d_ids, T, E);
@@ -331,7 +362,7 @@ extern "C" void gpt2_forward_noalloc(const GPT2Backend *be, const GPT2WeightsGPU
     s.fc = s.ao + t * E;
     s.ff = s.fc + t * GPT2_FFN_DIM;
     s.maxT = GPT2_NOALLOC_MAX_T;
-    gpt2_forward_cuda(be, w, d_ids, T, &s, caps);
+    forward_impl(be, w, d_ids, T, &s, caps, false);
 }
 
 // ============================================================================ KV cache

@@ -39,17 +39,6 @@ __device__ __forceinline__ int swz(int row, int c) {
     else return c ^ ((row >> 1) & 3);
 }
 
-// Sign-exact int8 -> fp16 for four packed bytes: (b ^ 0x80) is b + 128 in [1, 255]; the half with
-// bits 0x6400 | u is 1024 + u; subtracting 1152 leaves b.  Returns two f16x2 words (lo, hi).
-__device__ __forceinline__ void i8x4_to_f16x4(uint32_t w, uint32_t &lo, uint32_t &hi) {
-    const uint32_t u = w ^ 0x80808080u;
-    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x05010400u);
-    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x07030602u);
-    const f16x2 bias = {(f16)-1152.0f, (f16)-1152.0f};
-    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, a) + bias);
-    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, b) + bias);
-}
-
 // Map the linear work-group id onto a tile id so that each XCD owns a contiguous tile range.
 __device__ __forceinline__ int xcd_tile(int bid, int ntiles) {
     const int xcd = bid & 7, slot = bid >> 3;
@@ -271,22 +260,6 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(uint16_t *__restrict__ C, con
 //     are read;
 //   * one barrier per k-tile: the buffer refilled at step kt was last read at step kt-1.
 
-// Wait until at most `after` k-tiles of this wave's loads (L instructions each) are outstanding.
-template <int L, int MAXA>
-__device__ __forceinline__ void wait_tiles(int after) {
-    if constexpr (MAXA >= 0) {
-        if (after == MAXA) { wait_vm<L * MAXA>(); return; }
-        wait_tiles<L, MAXA - 1>(after);
-    }
-}
-
-__device__ __forceinline__ f16x8 i8x8_to_f16x8(uint2 w) {
-    uint32_t h[4];
-    i8x4_to_f16x4(w.x, h[0], h[1]);
-    i8x4_to_f16x4(w.y, h[2], h[3]);
-    const i32x4 v = {(int)h[0], (int)h[1], (int)h[2], (int)h[3]};
-    return __builtin_bit_cast(f16x8, v);
-}
 
 // KS > 1 splits the k-tiles inside the work-group: KS groups of WN x WM waves, each with its own LDS
 // ring, run the same pipeline over consecutive 1/KS shares of K (so their barriers line up), and

@@ -1,0 +1,160 @@
+"""The persistent prefill (csrc/prefill.hip: the 12-layer trunk as one kernel, tasks taken from a
+ticket in dependency order) against the per-op launch sequence of the same library and against the
+fp32 oracle.
+
+Bars: the oracle gates of the reference (per-layer rel_err <= 1e-2, logits rel_err <= 1e-2, max
+KL < 0.02; INT8 on the dequantized weights); against the launch sequence, which computes the same
+fp16 values with other tile shapes (other fp32 summation orders), rel_err <= 5e-3 on every capture
+and the K/V cache.  Run-to-run the kernel is deterministic (a task's result does not depend on which
+work-group runs it): bit-identical captures on repeated calls."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skip(reason="persistent prefill switched off: its first launch (T=1, fp16) never completed "
+                            "on MI355X and no cause has been shown; the case stays off the GPU until one is"),
+]
+
+V, E = 50257, 768
+
+
+def rel_err(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(got - ref).max() / (np.abs(ref).max() + 1e-9))
+
+
+def kl_rows(ref, got):
+    def logsm(x):
+        x = x.astype(np.float64)
+        m = x.max(axis=-1, keepdims=True)
+        return x - m - np.log(np.exp(x - m).sum(axis=-1, keepdims=True))
+    lr, lg = logsm(ref), logsm(got)
+    return (np.exp(lr) * (lr - lg)).sum(axis=-1)
+
+
+@pytest.fixture(scope="module")
+def model(pkg, synth):
+    m = pkg.Model(synth.make_body(seed=77, plain=False))
+    yield m
+    m.free()
+
+
+def prefill(pkg, L, model, backend, ids, persistent):
+    T = len(ids)
+    d_ids = pkg.Dev.from_numpy(np.asarray(ids, np.int32))
+    scr, kv = pkg.Scratch(T), pkg.KVCache(T)
+    logits, blocks, fin = pkg.Dev(T * V * 2), pkg.Dev(12 * T * E * 2), pkg.Dev(T * E * 2)
+    caps = pkg.GPT2CapsGPU()
+    caps.logits, caps.logits_all, caps.final_ln, caps.blocks = logits.ptr, 1, fin.ptr, blocks.ptr
+    L.gpt2_memset(kv.kv.data, 0, kv.kv.bytes)
+    L.gpt2_tune_prefill_persistent(1 if persistent else 0)
+    try:
+        L.gpt2_prefill_fill_cache(pkg.backend(backend), C.byref(model.gpu), C.byref(kv.kv), d_ids.ptr, T,
+                                  C.byref(scr.s), C.byref(caps))
+        L.gpt2_sync()
+        pkg.check("prefill persistent=%d" % persistent)
+        assert L.gpt2_prefill_status() == 0
+    finally:
+        L.gpt2_tune_prefill_persistent(1)
+    cache = np.empty(kv.kv.bytes // 2, np.uint16)
+    assert L.gpt2_d2h(cache.ctypes.data, kv.kv.data, cache.nbytes) == 0
+    out = {"blocks": blocks.numpy(np.uint16, (12, T, E)), "final_ln": fin.numpy(np.uint16, (T, E)),
+           "logits": logits.numpy(np.uint16, (T, V)), "kv": cache}
+    scr.free()
+    kv.free()
+    return out
+
+
+def f32(a):
+    return oracle.f16_to_f32(a)
+
+
+@pytest.mark.parametrize("backend", ["flash", "int8"])
+@pytest.mark.parametrize("T", [1, 17, 33, 64, 200, 512, 1024])
+def test_persistent_matches_launch_sequence(pkg, L, synth, model, backend, T):
+    ids = synth.token_ids(T, seed=T + 100)
+    if backend == "int8":
+        model.quantize()
+    try:
+        print(f"persistent prefill {backend} T={T}", flush=True)
+        got = prefill(pkg, L, model, backend, ids, True)
+        ref = prefill(pkg, L, model, backend, ids, False)
+        again = prefill(pkg, L, model, backend, ids, True)
+    finally:
+        if backend == "int8":
+            L.gpt2_quant_free(C.byref(model.q))
+            model.q = None
+            model.gpu.q = None
+    for Lyr in range(12):
+        assert rel_err(f32(got["blocks"][Lyr]), f32(ref["blocks"][Lyr])) <= 5e-3, Lyr
+    for k in ("final_ln", "logits"):
+        assert rel_err(f32(got[k]), f32(ref[k])) <= 5e-3, k
+    assert kl_rows(f32(ref["logits"]), f32(got["logits"])).max() < 2e-3
+    assert rel_err(f32(got["kv"]), f32(ref["kv"])) <= 5e-3
+    for k in got:
+        assert np.array_equal(got[k], again[k]), f"{k}: not deterministic"
+
+
+@pytest.mark.parametrize("backend,T", [("flash", 64), ("int8", 64), ("flash", 300)])
+def test_persistent_prefill_vs_oracle(pkg, L, synth, model, backend, T):
+    body = synth.make_body(seed=77, plain=False)
+    ref_body = oracle.fp16_view(body)
+    ids = synth.token_ids(T, seed=T + 5)
+    if backend == "int8":
+        off = synth.offsets()
+        for Lyr in range(12):
+            for name in ("qkv_w", "attn_proj_w", "fc_w", "proj_w"):
+                o, shape = off[f"h{Lyr}.{name}"]
+                n = int(np.prod(shape))
+                q, s, _ = oracle.quantize_fp16_view(body[o:o + n].reshape(shape))
+                ref_body[o:o + n] = oracle.dequantize(q, s).reshape(-1)
+        model.quantize()
+    try:
+        got = prefill(pkg, L, model, backend, ids, True)
+    finally:
+        if backend == "int8":
+            L.gpt2_quant_free(C.byref(model.q))
+            model.q = None
+            model.gpu.q = None
+    ref = oracle.forward(ref_body, ids, logits_all=True, want_blocks=True)
+    for Lyr in range(12):
+        assert rel_err(f32(got["blocks"][Lyr]), ref["blocks"][Lyr]) <= 1e-2, Lyr
+    assert rel_err(f32(got["final_ln"]), ref["final_ln"]) <= 1e-2
+    lg = f32(got["logits"])
+    assert rel_err(lg, ref["logits"]) <= 1e-2
+    assert kl_rows(ref["logits"], lg).max() < 0.02
+
+
+def test_persistent_timeout_is_reported(pkg, L, synth, model):
+    """Error path forced from the host: with a zero-round poll limit the first task that finds a
+    counter short gives up, every work-group leaves, gpt2_prefill_status reports it (and clears it),
+    and the next launch with the default limit is whole again (the last work-group cleared the
+    counters and the ticket)."""
+    T = 96
+    ids = synth.token_ids(T, seed=3)
+    d_ids = pkg.Dev.from_numpy(np.asarray(ids, np.int32))
+    scr, kv = pkg.Scratch(T), pkg.KVCache(T)
+    logits = pkg.Dev(V * 2)
+    caps = pkg.GPT2CapsGPU()
+    caps.logits, caps.logits_all = logits.ptr, 0
+    L.gpt2_prefill_status()
+    L.gpt2_tune_prefill_spin(0)
+    try:
+        L.gpt2_prefill_fill_cache(pkg.backend("flash"), C.byref(model.gpu), C.byref(kv.kv), d_ids.ptr, T,
+                                  C.byref(scr.s), C.byref(caps))
+        L.gpt2_sync()
+        assert L.gpt2_prefill_status() != 0
+    finally:
+        L.gpt2_tune_prefill_spin(-1)
+    assert L.gpt2_prefill_status() == 0   # cleared by the read
+    scr.free()
+    kv.free()
+    got = prefill(pkg, L, model, "flash", ids, True)
+    ref = prefill(pkg, L, model, "flash", ids, False)
+    assert rel_err(f32(got["logits"]), f32(ref["logits"])) <= 5e-3
