@@ -25,7 +25,8 @@ Also reported in the same JSON line:
   forward_t64   config 1 on the GPU: the fp16 forward at T=64 with logits for all 64 rows
   decode        GPT-2-124M decode tok/s @ctx=512: INT8 trunk + fp16 head, one hipGraph replay per
                 token, after a P=512 prefill (the prefill itself is timed too); plus the mean over
-                the 511-step greedy run
+                the 511-step greedy run, and (decode.cold) the same step with its weights cold:
+                four uploads of the model stepped round robin, 650 MB of weights past the 256 MB MALL
   cpu_baseline  the reference's own cpu/forward_cpu.c matmul (oracle/_ref, if built) or the oracle
                 restatement, on the same four GEMM shapes, on this host's cores
   cpu_forward_t64  config 1 on the CPU: the reference's forward at T=64 with logits_all (median of
@@ -34,6 +35,7 @@ Also reported in the same JSON line:
                 positions per token), tok/s beside the GPU decode leg
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras]
+       (--gemv-only and --decode-only run one leg, as the drivers of the committed counter profiles)
 """
 from __future__ import annotations
 
@@ -456,7 +458,10 @@ def cpu_model():
 
 
 # ------------------------------------------------------------------------------ decode (config 5)
-def bench_decode(B, steady_reps=64):
+def bench_decode(B, steady_reps=64, greedy=True, cold_copies=4, cold_reps=48):
+    """Config 5 decode: the P=512 prefill, then the step at pos 512 (multi-kernel graph, persistent
+    step, eager), the 511-step greedy run, and the persistent step with its weights cold (see
+    decode_cold)."""
     pkg, L = B.pkg, B.L
     synth = importlib.import_module("bare_metal_gpt2_amd.synth")
     t0 = time.time()
@@ -522,13 +527,16 @@ def bench_decode(B, steady_reps=64):
             eager.append((time.perf_counter() - t) * 1e3)
     pkg.check("eager decode")
     # the full greedy run: 511 steps from pos 512 (ctx 512 -> 1023)
-    kv.kv.len = P
-    L.gpt2_decode_graph_set(g, first, P)
-    L.gpt2_decode_graph_time(g, 511, C.byref(ms))
     tok, pos = C.c_int(), C.c_int()
-    if L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)):
+    greedy_ms = None
+    if greedy:
+        kv.kv.len = P
+        L.gpt2_decode_graph_set(g, first, P)
+        L.gpt2_decode_graph_time(g, 511, C.byref(ms))
+        if L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)):
+            pkg.check("greedy run")
         pkg.check("greedy run")
-    pkg.check("greedy run")
+        greedy_ms = ms.value
     L.gpt2_decode_graph_destroy(g)
     streamed = model.q.streamed_bytes
     kv_bytes = L.gpt2_kv_step_bytes(C.byref(kv.kv), P + 1)
@@ -540,14 +548,75 @@ def bench_decode(B, steady_reps=64):
            "ms_step_min_max": [round(min(samples), 4), round(max(samples), 4)],
            "multi_kernel_graph_tok_s_at_512": round(1000.0 / med_multi, 1),
            "eager_ms_step_at_512": round(float(np.median(eager)), 4),
-           "greedy_511_tok_s": round(1000.0 / ms.value, 1), "greedy_final_pos": pos.value,
+           "greedy_511_tok_s": round(1000.0 / greedy_ms, 1) if greedy_ms else None,
+           "greedy_final_pos": pos.value if greedy_ms else None,
            "weight_bytes": int(streamed), "kv_bytes_at_513": int(kv_bytes),
            "step_GBs_at_512": round((streamed + kv_bytes) / (med * 1e-3) / 1e9, 1),
            "setup_s": round(time.time() - t0, 1)}
-    scr.free()
     kv.free()
     model.free()
+    if cold_copies:
+        res["cold"] = decode_cold(B, scr, first, logits, tokens, streamed, kv_bytes, med, cold_copies, cold_reps)
+    scr.free()
     return res
+
+
+def decode_cold(B, scr, first, logits, tokens, streamed, kv_bytes, warm_ms, copies, reps):
+    """The persistent step with its weights cold: `copies` uploads of the same model, each with its own
+    K/V cache (the P=512 prefill) and graph, stepped round robin at pos 512, so the 162 MB of weights
+    a step reads were last read copies-1 steps (>= 487 MB of other weights) earlier, past the 256 MB
+    MALL.  The warm figure is the same step repeated on one copy."""
+    pkg, L = B.pkg, B.L
+    synth = importlib.import_module("bare_metal_gpt2_amd.synth")
+    P = 512
+    ids = synth.token_ids(P, seed=1234)
+    d_ids = B.dev(ids)
+    be = pkg.backend("int8")
+    caps = pkg.GPT2CapsGPU()
+    caps.logits = logits.ptr
+    caps.logits_all = 0
+    models, kvs, graphs = [], [], []
+    ms = C.c_float()
+    try:
+        for _ in range(copies):
+            m = pkg.Model(seeded_body())
+            m.quantize()
+            kv = pkg.KVCache(1024)
+            models.append(m)
+            kvs.append(kv)
+            L.gpt2_prefill_fill_cache(be, C.byref(m.gpu), C.byref(kv.kv), d_ids.ptr, P, C.byref(scr.s), C.byref(caps))
+            g = L.gpt2_decode_graph_create_mode(be, C.byref(m.gpu), C.byref(kv.kv), C.byref(scr.s), logits.ptr,
+                                                tokens.ptr, pkg.DECODE_AUTO)
+            if not g:
+                pkg.check("cold graph create")
+                raise RuntimeError("graph create failed")
+            graphs.append(g)
+        L.gpt2_sync()
+        pkg.check("cold setup")
+        samples = []
+        for i in range(reps + copies):
+            g = graphs[i % copies]
+            L.gpt2_decode_graph_set(g, first, P)
+            L.gpt2_decode_graph_time(g, 1, C.byref(ms))
+            if i >= copies:
+                samples.append(ms.value)
+        tok, pos = C.c_int(), C.c_int()
+        for g in graphs:
+            if L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)):
+                pkg.check("cold decode")
+        pkg.check("cold decode")
+        med = float(np.median(samples))
+        return {"copies": copies, "rotated_weight_MB": round(copies * streamed / 1e6, 1),
+                "ms_step_at_512": round(med, 4), "tok_s_at_512": round(1000.0 / med, 1),
+                "step_GBs_at_512": round((streamed + kv_bytes) / (med * 1e-3) / 1e9, 1),
+                "cold_over_warm": round(med / warm_ms, 3)}
+    finally:
+        for g in graphs:
+            L.gpt2_decode_graph_destroy(g)
+        for kv in kvs:
+            kv.free()
+        for m in models:
+            m.free()
 
 
 # ------------------------------------------------------------------------------ measured ceilings
@@ -597,6 +666,8 @@ def guard_legs(out, read_gbs):
     d = out.get("decode")
     if d:
         warm.append(("decode.step_GBs_at_512", d["step_GBs_at_512"]))
+        if d.get("cold"):
+            cold.append(("decode.cold.step_GBs_at_512", d["cold"]["step_GBs_at_512"]))
     sus = [{"leg": k, "GBs": v, "over_read_stream": round(v / read_gbs, 3)} for k, v in cold if v > read_gbs]
     return {"read_stream_GBs": read_gbs, "suspicious": sus,
             "cold_frac_of_read_stream": {k: round(v / read_gbs, 3) for k, v in cold},
@@ -714,6 +785,9 @@ def main():
                     help="only the decode GEMV legs (INT8 trunk cold/warm, the 48-GEMV chain, INT8 and fp16 head) "
                          "with a few launches each, printed as one JSON line: the driver for their rocprofv3 "
                          "counter runs")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the config-5 decode leg (prefill, step at pos 512 warm and with its weights cold; "
+                         "no greedy run), printed as one JSON line: the driver for the decode step's counter runs")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="also run one plain copy of BYTES (calibrates FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -746,6 +820,9 @@ def main():
     if args.gemv_only:
         gemv, head = bench_gemv(B, quick=True)
         print(json.dumps({"gemv_int8": gemv, "head_gemv_fp16": head}), flush=True)
+        return
+    if args.decode_only:
+        print(json.dumps({"decode": bench_decode(B, steady_reps=32, greedy=False)}), flush=True)
         return
     flops_step, ms_step, shapes, roofline, ms_graph = bench_gemm_set(B, args.steps, args.warmup)
     value = flops_step / (ms_step * 1e-3) / 1e12
