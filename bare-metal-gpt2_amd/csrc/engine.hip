@@ -260,8 +260,8 @@ static void forward_impl(const GPT2Backend *be, const GPT2WeightsGPU *w, const i
     if (kv && T > kv->maxT) { arg_fail("gpt2_forward_cuda: T exceeds the KV cache"); return; }
 
     const bool fused = fused_prefill_ok(be);
-    // The 12-layer trunk as one persistent kernel (prefill.hip; switched off, so prefill_persist
-    // returns nullptr and the launch sequence below runs); the final LayerNorm, the head and the
+    // With the persistent prefill switched on (off by default: slower than the launch sequence),
+    // the 12-layer trunk runs as one kernel (prefill.hip); the final LayerNorm, the head and the
     // captures follow as launches.
     if (fused && persistent) {
         const uint16_t *x0 = nullptr, *xl[GPT2_N_LAYER];

@@ -42,9 +42,9 @@ struct PFArgs {
 const uint16_t *prefill_persist(const GPT2Backend *be, const GPT2WeightsGPU *w, const int *d_ids, int T,
                                 GPT2KVCache *kv, const uint16_t **embed_out, const uint16_t **layer_out);
 
-// Test/tuning hooks: on/off switch (off, and refusing "on" while the kernel is switched off) and
-// the poll limit of later launches.
-void prefill_persist_enable(bool on);
+// Test/tuning hooks: on/off switch (1 on, 0 off, -1 the default: off) and the poll limit of later
+// launches.
+void prefill_persist_enable(int on);
 bool prefill_persist_enabled();
 
 }  // namespace g2

@@ -1,8 +1,5 @@
 // prefill.hip -- the prefill's 12-layer trunk as ONE persistent kernel (gfx950).
 //
-// STATUS: switched off (PF_AVAILABLE below).  Its first launch on MI355X did not complete and the
-// cause has not been found; prefills run the multi-launch sequence of engine.hip.
-//
 // Replaces the per-op launch sequence of the prefill forward (cuda/forward_cuda.cu:77-116: per layer
 // LayerNorm, QKV matmul, attention, attn-proj + residual, LayerNorm, fc + gelu, mlp-proj +
 // residual) for this library's backends.  Why: on MI355X each launch of a prefill-sized op costs
@@ -72,24 +69,29 @@ __device__ __forceinline__ void st_dev64(uint16_t *p, uint2 v) {
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Thread 0 polls until *c >= target; false after the poll limit or once another work-group has
-// recorded an error.
+// A value every lane of the wave holds alike, as a scalar: branches on it are wave-uniform in the
+// compiled code.
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Wave 0 polls (all its lanes load the same word; every branch is on a scalar copy) until
+// *c >= target; false after the poll limit or once another work-group has recorded an error.
 __device__ bool pf_poll(const uint32_t *c, uint32_t target, uint32_t *ctl, int spin) {
     for (int round = 0;; ++round) {
-        if (ld_dev(c) >= target) return true;
-        if (round >= spin || ((round & 31) == 31 && ld_dev(ctl + 2))) {
-            __hip_atomic_fetch_or(ctl + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (uni(ld_dev(c)) >= target) return true;
+        if (round >= spin || ((round & 31) == 31 && uni(ld_dev(ctl + 2)))) {
+            __hip_atomic_fetch_or(ctl + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // idempotent
             return false;
         }
         __builtin_amdgcn_s_sleep(1);
     }
 }
 
-// Every wave's stores have completed, then one increment of the task's counter.
-__device__ __forceinline__ void pf_signal(uint32_t *c) {
+// Every wave's stores have completed, then one increment of the task's counter (wave 0: lane 0 adds
+// one, the other lanes zero, so no lane branches).
+__device__ __forceinline__ void pf_signal(uint32_t *c, bool wave0, int lane) {
     wait_vm<0>();
     __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (wave0) __hip_atomic_fetch_add(c, lane == 0 ? 1u : 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------------------------------ GEMM tile
@@ -316,31 +318,42 @@ __global__ __launch_bounds__(PF_T) void k_prefill_persist(const PFArgs a) {
     __shared__ __attribute__((aligned(1024))) char lds[PF_LDS];
     uint32_t &s_task = reinterpret_cast<uint32_t *>(lds)[0];
     uint32_t &s_flag = reinterpret_cast<uint32_t *>(lds)[1];
+    // No branch on a path to a barrier may be lane-divergent in the compiled code.  With the ticket
+    // fetch, the polls and the counter bumps under `threadIdx.x == 0` (a loop-invariant condition
+    // that differs between the lanes of wave 0), the compiler routed the loop's back-edge around
+    // them: lanes 1-63 went from a task's end straight back to the barrier before the next task
+    // word, re-reading the old word, while thread 0 waited at the inner loop's exit for its own
+    // wave's other lanes -- the work-group re-ran its first task forever.  So wave 0 as a whole
+    // (a wave-uniform condition) fetches tickets, polls and signals, lane 0 alone adding one in
+    // each atomic; the broadcast words are read into scalar registers (uni), which makes the loop,
+    // its exits and the task dispatch uniform.
     static_assert(sizeof(AttnLds) <= PF_LDS, "attention LDS fits");
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const bool wave0 = __builtin_amdgcn_readfirstlane(tid >> 6) == 0;
     const int T = a.T, spin = a.spin;
     uint32_t *cnt = a.cnt, *ctl = a.ctl;
 
     for (;;) {
-        if (tid == 0) {
+        if (wave0) {
             uint32_t t = PF_NONE;
-            if (!ld_dev(ctl + 2)) {
-                const uint32_t k = __hip_atomic_fetch_add(ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (k < (uint32_t)a.ntasks) t = a.tasks[k];
+            if (!uni(ld_dev(ctl + 2))) {
+                const uint32_t k = uni(__hip_atomic_fetch_add(ctl, lane == 0 ? 1u : 0u, __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT));
+                if (k < (uint32_t)a.ntasks) t = uni(a.tasks[k]);
             }
-            s_task = t;
+            s_task = t;   // every lane of wave 0 writes the same word
         }
         __syncthreads();
-        const uint32_t tw = s_task;
+        const uint32_t tw = uni(s_task);
         __syncthreads();   // s_task is rewritten at the top of the next round
         if (tw == PF_NONE) break;
         const int type = (int)(tw & 15u), l = (int)((tw >> 4) & 15u), ta = (int)((tw >> 8) & 255u),
                   tb = (int)((tw >> 16) & 255u);
-        // one dependency wait: thread 0 polls the counters, every thread gets the outcome
+        // one dependency wait: wave 0 polls the counters, every thread gets the outcome
         auto wait_on = [&](auto &&poll_all) {
-            if (tid == 0) s_flag = poll_all() ? 1u : 0u;
+            if (wave0) s_flag = poll_all() ? 1u : 0u;
             __syncthreads();
-            const bool ok = s_flag != 0u;
+            const bool ok = uni(s_flag) != 0u;
             __syncthreads();
             return ok;
         };
@@ -362,7 +375,7 @@ __global__ __launch_bounds__(PF_T) void k_prefill_persist(const PFArgs a) {
                 st_dev64(x0 + (size_t)t * GPT2_N_EMBD + e, uint2{(uint32_t)o[0] | ((uint32_t)o[1] << 16),
                                                                  (uint32_t)o[2] | ((uint32_t)o[3] << 16)});
             }
-            pf_signal(cnt + cidx(0, ST_X, rb));
+            pf_signal(cnt + cidx(0, ST_X, rb), wave0, lane);
         } else if (type == TK_ATT) {
             const PFLayer &ly = a.layers[l];
             const int h = ta, q0 = tb * AP_QB;
@@ -374,7 +387,7 @@ __global__ __launch_bounds__(PF_T) void k_prefill_persist(const PFArgs a) {
             });
             if (ok) {
                 attn_block<true>(*reinterpret_cast<AttnLds *>(lds), ly.att, ly.qkv, T, ly.kc, ly.vc, a.maxT, h, q0);
-                pf_signal(cnt + cidx(l, ST_ATT, q0 / PF_RB));
+                pf_signal(cnt + cidx(l, ST_ATT, q0 / PF_RB), wave0, lane);
             }
         } else {
             const PFLayer &ly = a.layers[l];
@@ -385,7 +398,7 @@ __global__ __launch_bounds__(PF_T) void k_prefill_persist(const PFArgs a) {
                     lds, [&] { return wait_on([&] { return pf_poll(cnt + cidx(l, ST_X, rb), need, ctl, spin); }); },
                     ly.x_in, GPT2_N_EMBD, ly.ln1_g, ly.ln1_b, ly.w[0], ly.s[0], ly.b[0], nullptr, ly.qkv, GPT2_QKV_DIM, m0,
                     64 * tb, T);
-                if (ok) pf_signal(cnt + cidx(l, ST_QKV, rb));
+                if (ok) pf_signal(cnt + cidx(l, ST_QKV, rb), wave0, lane);
             } else if (type == TK_PROJ) {
                 const int nqb = (min(m0 + PF_RB, T) - m0 + AP_QB - 1) / AP_QB;
                 ok = pf_gemm<64, false, Q8, EPI_RESID>(
@@ -393,34 +406,35 @@ __global__ __launch_bounds__(PF_T) void k_prefill_persist(const PFArgs a) {
                     [&] { return wait_on([&] { return pf_poll(cnt + cidx(l, ST_ATT, rb), (uint32_t)(GPT2_N_HEAD * nqb), ctl, spin); }); },
                     ly.att, GPT2_N_EMBD, nullptr, nullptr, ly.w[1], ly.s[1], ly.b[1], ly.x_in, ly.mid, GPT2_N_EMBD, m0,
                     64 * tb, T);
-                if (ok) pf_signal(cnt + cidx(l, ST_MID, rb));
+                if (ok) pf_signal(cnt + cidx(l, ST_MID, rb), wave0, lane);
             } else if (type == TK_FC) {
                 ok = pf_gemm<64, true, Q8, EPI_GELU>(
                     lds, [&] { return wait_on([&] { return pf_poll(cnt + cidx(l, ST_MID, rb), N_PROJ, ctl, spin); }); },
                     ly.mid, GPT2_N_EMBD, ly.ln2_g, ly.ln2_b, ly.w[2], ly.s[2], ly.b[2], nullptr, ly.h, GPT2_FFN_DIM, m0,
                     64 * tb, T);
-                if (ok) pf_signal(cnt + cidx(l, ST_H, rb));
+                if (ok) pf_signal(cnt + cidx(l, ST_H, rb), wave0, lane);
             } else {   // TK_MLP
                 ok = pf_gemm<32, false, Q8, EPI_RESID>(
                     lds, [&] { return wait_on([&] { return pf_poll(cnt + cidx(l, ST_H, rb), N_FC, ctl, spin); }); },
                     ly.h, GPT2_FFN_DIM, nullptr, nullptr, ly.w[3], ly.s[3], ly.b[3], ly.mid, ly.x_out, GPT2_N_EMBD, m0,
                     32 * tb, T);
-                if (ok) pf_signal(cnt + cidx(l + 1, ST_X, rb));
+                if (ok) pf_signal(cnt + cidx(l + 1, ST_X, rb), wave0, lane);
             }
         }
         if (!ok) break;   // uniform: every thread saw the same wait outcome
     }
     // The last work-group to leave clears the counters and the ticket for the next launch.
     __syncthreads();
-    if (tid == 0) s_flag = __hip_atomic_fetch_add(ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (wave0) s_flag = uni(__hip_atomic_fetch_add(ctl + 1, lane == 0 ? 1u : 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     __syncthreads();
-    if (s_flag == gridDim.x - 1) {
+    if (uni(s_flag) == gridDim.x - 1) {
         for (int i = tid; i < PF_NCNT; i += PF_T) __hip_atomic_store(cnt + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         wait_vm<0>();
         __syncthreads();
-        if (tid == 0) {
-            // an error of this launch moves to the sticky status word (read by gpt2_prefill_status)
-            const uint32_t e = ld_dev(ctl + 2);
+        if (wave0) {
+            // an error of this launch moves to the sticky status word (read by gpt2_prefill_status);
+            // every lane of wave 0 performs the same stores (and an idempotent OR)
+            const uint32_t e = uni(ld_dev(ctl + 2));
             if (e) __hip_atomic_fetch_or(ctl + 3, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(ctl + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(ctl, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -431,11 +445,10 @@ __global__ __launch_bounds__(PF_T) void k_prefill_persist(const PFArgs a) {
 
 // ------------------------------------------------------------------------------ host side
 namespace {
-// Switched off, and it cannot be switched on: the first launch on MI355X (T = 1, fp16 weights)
-// never completed, and no cause has been shown (every poll in the kernel is bounded, so a wait on
-// a counter cannot explain it).  Until one is, prefills run the multi-launch sequence.
-constexpr bool PF_AVAILABLE = false;
-bool g_enabled = false;
+// Off by default: correct (the launch sequence's results within the fp16 gates, deterministic), but
+// slower than the multi-launch prefill it replaces (P=512 INT8: 1.74 against 0.65 ms).
+constexpr bool PF_DEFAULT = false;
+bool g_enabled = PF_DEFAULT;
 int g_spin = PF_SPIN;
 
 struct Arena {
@@ -516,13 +529,7 @@ bool arena_ready(int T, bool q8) {
 }
 }  // namespace
 
-void prefill_persist_enable(bool on) {
-    if (on && !PF_AVAILABLE) {
-        set_error(E_STATE, "persistent prefill is switched off (its first launch did not complete; cause not found)");
-        return;
-    }
-    g_enabled = on;
-}
+void prefill_persist_enable(int on) { g_enabled = on < 0 ? PF_DEFAULT : on != 0; }
 bool prefill_persist_enabled() { return g_enabled; }
 
 const uint16_t *prefill_persist(const GPT2Backend *be, const GPT2WeightsGPU *w, const int *d_ids, int T,
@@ -606,9 +613,9 @@ const uint16_t *prefill_persist(const GPT2Backend *be, const GPT2WeightsGPU *w, 
 }  // namespace g2
 
 // Test / tuning hooks (not part of the reference interface).
-// 0 makes every prefill run the multi-launch sequence (the default); 1 would select the persistent
-// kernel, but while it is switched off the call records an error (E_STATE) and changes nothing.
-extern "C" void gpt2_tune_prefill_persistent(int on) { g2::prefill_persist_enable(on != 0); }
+// 1 makes every later prefill of this library's backends run the persistent kernel, 0 the
+// multi-launch sequence, -1 the default (the multi-launch sequence).
+extern "C" void gpt2_tune_prefill_persistent(int on) { g2::prefill_persist_enable(on); }
 // Poll rounds before a persistent-prefill work-group gives up, for later launches (< 0: default;
 // 0 gives up at the first poll that finds a counter short -- forces the error path with every
 // kernel still exiting normally).

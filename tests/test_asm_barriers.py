@@ -1,0 +1,107 @@
+"""Compiled-code check of the persistent kernels (work-groups that wait on each other): no loop may
+narrow EXEC on its way back to its header (a lane-divergent latch) while a barrier lies inside it.
+
+Why: such a loop lets some lanes of a wave cycle back to a barrier while the wave's other lanes wait
+at the loop's exit for them.  The persistent prefill once compiled that way: with the ticket fetch and
+the counter bumps under `threadIdx.x == 0`, lanes 1-63 of wave 0 (and waves 1-3) went from a task's
+end straight back to the barrier before the next task word, re-reading the old one, while thread 0
+waited -- the work-group re-ran its first task forever.  The kernels now branch only on wave-uniform
+values around barriers; this test compiles them (hipcc -S, the flags of csrc/Makefile) and reads the
+loop structure from the compiler's block comments.  CPU only: it needs hipcc, not a GPU."""
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(ROOT, "bare-metal-gpt2_amd", "csrc")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+FLAGS = ["-O3", "-std=c++17", "--offload-arch=gfx950", "-I" + os.path.join(ROOT, "include"),
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S"]
+EXTRA = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}   # as in csrc/Makefile
+
+
+def blocks(lines):
+    out, cur = [], None
+    for i, line in enumerate(lines):
+        m = re.match(r"^(\.LBB\d+_\d+|; %bb\.\d+):", line)
+        if m:
+            name = m.group(1) if m.group(1).startswith(".LBB") else f"bb@{i}"
+            cur = {"name": name, "lines": []}
+            out.append(cur)
+        if cur is not None:
+            cur["lines"].append(line)
+    return out
+
+
+def hazardous_loops(asm):
+    """Loops (by header) with a lane-divergent latch and a barrier inside (nested loops included)."""
+    bs = blocks(asm.splitlines())
+    parent, inner = {}, {}
+    for b in bs:
+        head = "\n".join(b["lines"][:12])
+        if re.search(r"This (?:Inner )?Loop Header: Depth=\d+", head):
+            name = b["name"].lstrip(".").replace("LBB", "BB")
+            parents = re.findall(r"Parent Loop (BB\d+_\d+) Depth=\d+", head)
+            parent[name] = parents[-1] if parents else None
+            inner[b["name"]] = name
+        else:
+            m = re.search(r"in Loop: Header=(BB\d+_\d+) Depth", head)
+            inner[b["name"]] = m.group(1) if m else None
+
+    def within(loop, target):
+        while loop:
+            if loop == target:
+                return True
+            loop = parent.get(loop)
+        return False
+
+    bad = []
+    for loop in parent:
+        label = "." + loop.replace("BB", "LBB")
+        members = [k for k, b in enumerate(bs) if within(inner[b["name"]], loop)]
+        barrier = any(x.strip().startswith("s_barrier") for k in members for x in bs[k]["lines"])
+        divergent = False
+        for k in members:
+            body = "\n".join(bs[k]["lines"])
+            jumps = re.search(r"^\s*s_c?branch\w* " + re.escape(label) + r"\s*$", body, re.M)
+            falls = k + 1 < len(bs) and bs[k + 1]["name"] == label and not re.match(r"\s*s_branch ", bs[k]["lines"][-1])
+            if (jumps or falls) and re.search(r"^\s*s_andn2_b64 exec, exec,", body, re.M):
+                divergent = True
+        if divergent and barrier:
+            bad.append(loop)
+    return bad
+
+
+def test_scanner_flags_the_known_pattern():
+    """The check itself: a loop whose latch narrows EXEC back to a header with a barrier is flagged,
+    the same loop with a scalar latch is not."""
+    def listing(latch):
+        return "\n".join([
+            ".LBB0_1:                                ; =>This Loop Header: Depth=1",
+            "\ts_barrier",
+            "\tds_read_b32 v2, v3",
+            "; %bb.2:                                ;   in Loop: Header=BB0_1 Depth=1",
+            latch,
+            "\ts_cbranch_execnz .LBB0_1",
+            "; %bb.3:",
+            "\ts_endpgm",
+        ])
+    assert hazardous_loops(listing("\ts_andn2_b64 exec, exec, s[4:5]")) == ["BB0_1"]
+    assert hazardous_loops(listing("\ts_and_b64 vcc, exec, s[4:5]")) == []
+
+
+@pytest.mark.parametrize("src", ["prefill.hip", "decode.hip"])
+def test_persistent_kernels_have_uniform_loops_around_barriers(src, tmp_path):
+    if not shutil.which(HIPCC) and not os.path.exists(HIPCC):
+        pytest.skip("hipcc not available")
+    out = tmp_path / (src + ".s")
+    r = subprocess.run([HIPCC, *FLAGS, *EXTRA.get(src, []), os.path.join(CSRC, src), "-o", str(out)],
+                       capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-2000:]
+    asm = out.read_text()
+    assert "s_barrier" in asm and "Loop Header" in asm
+    assert hazardous_loops(asm) == []

@@ -119,14 +119,16 @@ def test_prefill_forward_backends_agree(pkg, L, synth, model):
 
 @pytest.mark.parametrize("backend,T", [("flash", 200), ("int8", 200), ("tiled", 33), ("int8", 512)])
 def test_fused_prefill_bit_identical(pkg, L, synth, model, backend, T):
-    """The fused prefill (gelu and the residual adds in GEMM epilogues, the K/V cache fill inside the
-    attention launch) equals the unfused reference sequence bit for bit: every layer's residual
-    stream, the final LayerNorm, all logits rows and the whole K/V cache."""
+    """The fused launch sequence of the prefill (gelu and the residual adds in GEMM epilogues, the K/V
+    cache fill inside the attention launch; the persistent trunk kernel switched off) equals the
+    unfused reference sequence bit for bit: every layer's residual stream, the final LayerNorm, all
+    logits rows and the whole K/V cache."""
     ids = synth.token_ids(T, seed=T + 7)
     d_ids = pkg.Dev.from_numpy(np.asarray(ids, np.int32))
     if backend == "int8":
         model.quantize()
     runs = []
+    L.gpt2_tune_prefill_persistent(0)
     try:
         for fused in (1, 0):
             L.gpt2_tune_prefill_fused(fused)
@@ -148,6 +150,7 @@ def test_fused_prefill_bit_identical(pkg, L, synth, model, backend, T):
             kv.free()
     finally:
         L.gpt2_tune_prefill_fused(1)
+        L.gpt2_tune_prefill_persistent(-1)
         if backend == "int8":
             L.gpt2_quant_free(C.byref(model.q))
             model.q = None

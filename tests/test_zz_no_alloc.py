@@ -1,13 +1,17 @@
 """gpt2_forward_noalloc (the forward with its activations in a static device array, no allocation)
-against gpt2_forward_cuda (the same forward on an allocated GPT2ScratchGPU): identical kernels in the
-same order, so every capture must match bit for bit -- all logits rows, the final LayerNorm, every
-layer's residual stream and the K/V cache it fills.  Two calls in a row, the second with fewer
-tokens (the array keeps the first call's contents), for the fp16 and the INT8 backend; and a call
-past the static limit is refused with an error and writes nothing."""
+against gpt2_forward_cuda (the same forward on an allocated GPT2ScratchGPU).  The no-allocation entry
+point runs the per-op launch sequence (the persistent trunk kernel allocates its arena on first use),
+so it matches gpt2_forward_cuda with that kernel switched off (the default) bit for bit -- all logits
+rows, the final LayerNorm, every layer's residual stream and the K/V cache it fills -- and
+gpt2_forward_cuda with the persistent kernel switched on within the fp16 gates.  Two calls in a row, the second with fewer tokens
+(the array keeps the first call's contents), for the fp16 and the INT8 backend; and a call past the
+static limit is refused with an error and writes nothing."""
 import ctypes as C
 
 import numpy as np
 import pytest
+
+import oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -57,9 +61,21 @@ def test_forward_noalloc_matches_forward(pkg, L, synth, model, backend):
             ids = synth.token_ids(T, seed=T + 3)
             print(f"forward_noalloc backend={backend} T={T}", flush=True)
             got = run(pkg, L, model, backend, ids, noalloc=True)
-            ref = run(pkg, L, model, backend, ids, noalloc=False)
+            L.gpt2_tune_prefill_persistent(0)
+            try:
+                ref = run(pkg, L, model, backend, ids, noalloc=False)
+            finally:
+                L.gpt2_tune_prefill_persistent(-1)
             for name, a, b in zip(("logits", "final_ln", "blocks", "kv"), got, ref):
                 assert np.array_equal(a, b), f"{backend} T={T}: {name} differs in {np.count_nonzero(a != b)} elements"
+            L.gpt2_tune_prefill_persistent(1)
+            try:
+                pers = run(pkg, L, model, backend, ids, noalloc=False)
+            finally:
+                L.gpt2_tune_prefill_persistent(-1)
+            for name, a, b in zip(("logits", "final_ln", "blocks"), got, pers):
+                fa, fb = oracle.f16_to_f32(a).astype(np.float64), oracle.f16_to_f32(b).astype(np.float64)
+                assert np.abs(fa - fb).max() / (np.abs(fb).max() + 1e-9) <= 1e-2, (backend, T, name)
     finally:
         if backend == "int8":
             L.gpt2_quant_free(C.byref(model.q))
