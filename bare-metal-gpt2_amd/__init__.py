@@ -181,6 +181,7 @@ SIGNATURES = {
     "gpt2_tune_prefill_persistent": (None, [_i]),
     "gpt2_tune_prefill_spin": (None, [_i]),
     "gpt2_prefill_status": (_i, []),
+    "gpt2_tune_prefill_trace": (_i, [_vp, _i, _i]),
     "gpt2_tune_gemm_pick_q": (_i, [_i, _i, _i, _i]),
     "gpt2_tune_gemm_fits": (_i, [_i, _i]),
     "gpt2_tune_gemm_force": (None, [_i]),

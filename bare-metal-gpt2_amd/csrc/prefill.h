@@ -32,6 +32,7 @@ struct PFArgs {
     uint32_t *ctl;           // {ticket, work-groups done, error of this launch, sticky error status}
     int T, maxT, ntasks;
     int spin;                // poll rounds before a work-group gives up
+    uint64_t *trace;         // optional: 8 words per ticket (work-group and 7 timestamps)
 };
 
 // Runs the 12-layer trunk of a T-token prefill as one kernel: embedding, then per layer LN1 + QKV,

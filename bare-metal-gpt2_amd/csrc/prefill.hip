@@ -53,6 +53,10 @@ enum { TK_EMB = 0, TK_QKV = 1, TK_ATT = 2, TK_PROJ = 3, TK_FC = 4, TK_MLP = 5 };
 constexpr int PF_NCNT = (GPT2_N_LAYER + 1) * PF_NST * PF_MAXRB;
 constexpr int PF_SPIN = 1 << 16;                   // default poll rounds before a work-group gives up
 constexpr uint32_t PF_NONE = 0xffffffffu;
+// Every atomic on a ticket or counter is made by all 64 lanes of wave 0 with the same value 1 (a
+// uniform value: the compiler folds it into one atomic of +64, where a per-lane 0/1 value costs a
+// 64-step scalar loop), so tickets and counters count in units of PF_ONE.
+constexpr uint32_t PF_ONE = 64;
 
 __host__ __device__ constexpr int cidx(int l, int st, int rb) { return (l * PF_NST + st) * PF_MAXRB + rb; }
 __host__ __device__ constexpr uint32_t task_word(int type, int l, int a, int b) {
@@ -86,12 +90,14 @@ __device__ bool pf_poll(const uint32_t *c, uint32_t target, uint32_t *ctl, int s
     }
 }
 
-// Every wave's stores have completed, then one increment of the task's counter (wave 0: lane 0 adds
-// one, the other lanes zero, so no lane branches).
-__device__ __forceinline__ void pf_signal(uint32_t *c, bool wave0, int lane) {
+// Every wave's stores have completed, then one increment of the task's counter (PF_ONE: every lane
+// of wave 0 adds one).
+__device__ __forceinline__ void pf_signal(uint32_t *c, bool wave0, uint64_t *tr) {
+    if (wave0 && tr) tr[5] = __builtin_amdgcn_s_memrealtime();   // trace: the task's stores are issued
     wait_vm<0>();
     __syncthreads();
-    if (wave0) __hip_atomic_fetch_add(c, lane == 0 ? 1u : 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (wave0 && tr) tr[6] = __builtin_amdgcn_s_memrealtime();   // trace: ... and have completed
+    if (wave0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // + PF_ONE
 }
 
 // ------------------------------------------------------------------------------------ GEMM tile
@@ -170,7 +176,7 @@ __device__ __forceinline__ void ln_panel(char *panel, const uint16_t *X, const u
 template <int BN, bool PANEL, bool QW, int EPI, class Deps>
 __device__ bool pf_gemm(char *lds, Deps deps, const uint16_t *A, int K, const uint16_t *ln_g,
                         const uint16_t *ln_b, const void *Wv, const float *Ws, const uint16_t *bias,
-                        const uint16_t *resid, uint16_t *C, int N, int m0, int n0, int T) {
+                        const uint16_t *resid, uint16_t *C, int N, int m0, int n0, int T, uint64_t *tr) {
     using G = TileGeo<BN, PANEL, QW>;
     constexpr int S = G::S, BK = G::BK, LMAX = G::LMAX, LO = G::LO, REM = G::REM, TM = G::TM;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -253,6 +259,7 @@ __device__ bool pf_gemm(char *lds, Deps deps, const uint16_t *A, int K, const ui
     f32x4 acc[TM];
 #pragma unroll
     for (int b = 0; b < TM; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (wave == 0 && tr) tr[3] = __builtin_amdgcn_s_memrealtime();   // trace: k-loop starts
     auto mfma_tile = [&](int kt) {
         const char *st = ring + (kt % S) * G::STAGE;
         const char *ab = PANEL ? panel + kt * 4096 : st;
@@ -290,6 +297,7 @@ __device__ bool pf_gemm(char *lds, Deps deps, const uint16_t *A, int K, const ui
         lds_barrier();
         mfma_tile(kt);
     }
+    if (wave == 0 && tr) tr[4] = __builtin_amdgcn_s_memrealtime();   // trace: k-loop done
     // epilogue: lane holds D[n][m] for n = nb .. nb+3, m = m0 + wm0 + 16 b + lrow
 #pragma unroll
     for (int b = 0; b < TM; ++b) {
@@ -324,22 +332,29 @@ __global__ __launch_bounds__(PF_T) void k_prefill_persist(const PFArgs a) {
     // them: lanes 1-63 went from a task's end straight back to the barrier before the next task
     // word, re-reading the old word, while thread 0 waited at the inner loop's exit for its own
     // wave's other lanes -- the work-group re-ran its first task forever.  So wave 0 as a whole
-    // (a wave-uniform condition) fetches tickets, polls and signals, lane 0 alone adding one in
-    // each atomic; the broadcast words are read into scalar registers (uni), which makes the loop,
-    // its exits and the task dispatch uniform.
+    // (a wave-uniform condition) fetches tickets, polls and signals (every lane adding one: units of
+    // PF_ONE); the broadcast words are read into scalar registers (uni), which makes the loop, its
+    // exits and the task dispatch uniform.
     static_assert(sizeof(AttnLds) <= PF_LDS, "attention LDS fits");
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x;
     const bool wave0 = __builtin_amdgcn_readfirstlane(tid >> 6) == 0;
     const int T = a.T, spin = a.spin;
     uint32_t *cnt = a.cnt, *ctl = a.ctl;
+    // optional per-task trace, 8 words per ticket (wave 0 writes it; every lane stores the same word,
+    // so nothing branches per lane): work-group, then s_memrealtime (100 MHz) when the task word
+    // arrived, its inputs were ready, a GEMM's k-loop started and ended, its stores were issued and had
+    // completed, and its counter was bumped (0: no such point)
+    uint64_t *tr = nullptr;
 
     for (;;) {
         if (wave0) {
             uint32_t t = PF_NONE;
             if (!uni(ld_dev(ctl + 2))) {
-                const uint32_t k = uni(__hip_atomic_fetch_add(ctl, lane == 0 ? 1u : 0u, __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_AGENT));
-                if (k < (uint32_t)a.ntasks) t = uni(a.tasks[k]);
+                const uint32_t k = uni(__hip_atomic_fetch_add(ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) / PF_ONE;
+                if (k < (uint32_t)a.ntasks) {
+                    t = uni(a.tasks[k]);
+                    tr = a.trace ? a.trace + 8 * (size_t)k : nullptr;
+                }
             }
             s_task = t;   // every lane of wave 0 writes the same word
         }
@@ -347,11 +362,19 @@ __global__ __launch_bounds__(PF_T) void k_prefill_persist(const PFArgs a) {
         const uint32_t tw = uni(s_task);
         __syncthreads();   // s_task is rewritten at the top of the next round
         if (tw == PF_NONE) break;
+        if (wave0 && tr) {
+            tr[0] = blockIdx.x;
+            tr[1] = __builtin_amdgcn_s_memrealtime();
+            tr[2] = tr[3] = tr[4] = 0;
+        }
         const int type = (int)(tw & 15u), l = (int)((tw >> 4) & 15u), ta = (int)((tw >> 8) & 255u),
                   tb = (int)((tw >> 16) & 255u);
         // one dependency wait: wave 0 polls the counters, every thread gets the outcome
         auto wait_on = [&](auto &&poll_all) {
-            if (wave0) s_flag = poll_all() ? 1u : 0u;
+            if (wave0) {
+                s_flag = poll_all() ? 1u : 0u;
+                if (tr) tr[2] = __builtin_amdgcn_s_memrealtime();
+            }
             __syncthreads();
             const bool ok = uni(s_flag) != 0u;
             __syncthreads();
@@ -375,57 +398,58 @@ __global__ __launch_bounds__(PF_T) void k_prefill_persist(const PFArgs a) {
                 st_dev64(x0 + (size_t)t * GPT2_N_EMBD + e, uint2{(uint32_t)o[0] | ((uint32_t)o[1] << 16),
                                                                  (uint32_t)o[2] | ((uint32_t)o[3] << 16)});
             }
-            pf_signal(cnt + cidx(0, ST_X, rb), wave0, lane);
+            pf_signal(cnt + cidx(0, ST_X, rb), wave0, tr);
         } else if (type == TK_ATT) {
             const PFLayer &ly = a.layers[l];
             const int h = ta, q0 = tb * AP_QB;
             const int rlast = (min(q0 + AP_QB, T) - 1) / PF_RB;
             ok = wait_on([&] {
                 for (int r = 0; r <= rlast; ++r)
-                    if (!pf_poll(cnt + cidx(l, ST_QKV, r), N_QKV, ctl, spin)) return false;
+                    if (!pf_poll(cnt + cidx(l, ST_QKV, r), N_QKV * PF_ONE, ctl, spin)) return false;
                 return true;
             });
             if (ok) {
                 attn_block<true>(*reinterpret_cast<AttnLds *>(lds), ly.att, ly.qkv, T, ly.kc, ly.vc, a.maxT, h, q0);
-                pf_signal(cnt + cidx(l, ST_ATT, q0 / PF_RB), wave0, lane);
+                pf_signal(cnt + cidx(l, ST_ATT, q0 / PF_RB), wave0, tr);
             }
         } else {
             const PFLayer &ly = a.layers[l];
             const int rb = ta, m0 = rb * PF_RB;
             if (type == TK_QKV) {
-                const uint32_t need = l == 0 ? 1u : (uint32_t)N_MLP;
+                const uint32_t need = (l == 0 ? 1u : (uint32_t)N_MLP) * PF_ONE;
                 ok = pf_gemm<64, true, Q8, EPI_NONE>(
                     lds, [&] { return wait_on([&] { return pf_poll(cnt + cidx(l, ST_X, rb), need, ctl, spin); }); },
                     ly.x_in, GPT2_N_EMBD, ly.ln1_g, ly.ln1_b, ly.w[0], ly.s[0], ly.b[0], nullptr, ly.qkv, GPT2_QKV_DIM, m0,
-                    64 * tb, T);
-                if (ok) pf_signal(cnt + cidx(l, ST_QKV, rb), wave0, lane);
+                    64 * tb, T, tr);
+                if (ok) pf_signal(cnt + cidx(l, ST_QKV, rb), wave0, tr);
             } else if (type == TK_PROJ) {
                 const int nqb = (min(m0 + PF_RB, T) - m0 + AP_QB - 1) / AP_QB;
                 ok = pf_gemm<64, false, Q8, EPI_RESID>(
                     lds,
-                    [&] { return wait_on([&] { return pf_poll(cnt + cidx(l, ST_ATT, rb), (uint32_t)(GPT2_N_HEAD * nqb), ctl, spin); }); },
+                    [&] { return wait_on([&] { return pf_poll(cnt + cidx(l, ST_ATT, rb), (uint32_t)(GPT2_N_HEAD * nqb) * PF_ONE, ctl, spin); }); },
                     ly.att, GPT2_N_EMBD, nullptr, nullptr, ly.w[1], ly.s[1], ly.b[1], ly.x_in, ly.mid, GPT2_N_EMBD, m0,
-                    64 * tb, T);
-                if (ok) pf_signal(cnt + cidx(l, ST_MID, rb), wave0, lane);
+                    64 * tb, T, tr);
+                if (ok) pf_signal(cnt + cidx(l, ST_MID, rb), wave0, tr);
             } else if (type == TK_FC) {
                 ok = pf_gemm<64, true, Q8, EPI_GELU>(
-                    lds, [&] { return wait_on([&] { return pf_poll(cnt + cidx(l, ST_MID, rb), N_PROJ, ctl, spin); }); },
+                    lds, [&] { return wait_on([&] { return pf_poll(cnt + cidx(l, ST_MID, rb), N_PROJ * PF_ONE, ctl, spin); }); },
                     ly.mid, GPT2_N_EMBD, ly.ln2_g, ly.ln2_b, ly.w[2], ly.s[2], ly.b[2], nullptr, ly.h, GPT2_FFN_DIM, m0,
-                    64 * tb, T);
-                if (ok) pf_signal(cnt + cidx(l, ST_H, rb), wave0, lane);
+                    64 * tb, T, tr);
+                if (ok) pf_signal(cnt + cidx(l, ST_H, rb), wave0, tr);
             } else {   // TK_MLP
                 ok = pf_gemm<32, false, Q8, EPI_RESID>(
-                    lds, [&] { return wait_on([&] { return pf_poll(cnt + cidx(l, ST_H, rb), N_FC, ctl, spin); }); },
+                    lds, [&] { return wait_on([&] { return pf_poll(cnt + cidx(l, ST_H, rb), N_FC * PF_ONE, ctl, spin); }); },
                     ly.h, GPT2_FFN_DIM, nullptr, nullptr, ly.w[3], ly.s[3], ly.b[3], ly.mid, ly.x_out, GPT2_N_EMBD, m0,
-                    32 * tb, T);
-                if (ok) pf_signal(cnt + cidx(l + 1, ST_X, rb), wave0, lane);
+                    32 * tb, T, tr);
+                if (ok) pf_signal(cnt + cidx(l + 1, ST_X, rb), wave0, tr);
             }
         }
+        if (wave0 && tr) tr[7] = __builtin_amdgcn_s_memrealtime();
         if (!ok) break;   // uniform: every thread saw the same wait outcome
     }
     // The last work-group to leave clears the counters and the ticket for the next launch.
     __syncthreads();
-    if (wave0) s_flag = uni(__hip_atomic_fetch_add(ctl + 1, lane == 0 ? 1u : 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    if (wave0) s_flag = uni(__hip_atomic_fetch_add(ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) / PF_ONE;
     __syncthreads();
     if (uni(s_flag) == gridDim.x - 1) {
         for (int i = tid; i < PF_NCNT; i += PF_T) __hip_atomic_store(cnt + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -450,6 +474,8 @@ namespace {
 constexpr bool PF_DEFAULT = false;
 bool g_enabled = PF_DEFAULT;
 int g_spin = PF_SPIN;
+uint64_t *g_trace = nullptr;   // per-task trace buffer (test/tuning hook) and its capacity in tasks
+int g_trace_cap = 0;
 
 struct Arena {
     int dev = -1, maxT = 0;
@@ -603,6 +629,7 @@ const uint16_t *prefill_persist(const GPT2Backend *be, const GPT2WeightsGPU *w, 
     a.maxT = kv && kv->data ? kv->maxT : T;
     a.ntasks = A.ntasks;
     a.spin = g_spin;
+    a.trace = (g_trace && g_trace_cap >= A.ntasks) ? g_trace : nullptr;
     if (q8) hipLaunchKernelGGL(k_prefill_persist<true>, dim3(A.grid), dim3(PF_T), 0, stream(), a);
     else hipLaunchKernelGGL(k_prefill_persist<false>, dim3(A.grid), dim3(PF_T), 0, stream(), a);
     check_launch("k_prefill_persist");
@@ -620,6 +647,16 @@ extern "C" void gpt2_tune_prefill_persistent(int on) { g2::prefill_persist_enabl
 // 0 gives up at the first poll that finds a counter short -- forces the error path with every
 // kernel still exiting normally).
 extern "C" void gpt2_tune_prefill_spin(int rounds) { g2::g_spin = rounds >= 0 ? rounds : g2::PF_SPIN; }
+// Per-task trace of later launches into buf (device memory, 8 x uint64 per task: work-group, then
+// s_memrealtime at the task's start, inputs ready, GEMM k-loop start and end, stores issued, stores
+// complete, counter bumped; 0 where a task has no such point); a launch with more tasks than cap is
+// not traced.  buf = nullptr stops tracing.  Returns the task count of
+// a T-token prefill.
+extern "C" int gpt2_tune_prefill_trace(unsigned long long *buf, int cap, int T) {
+    g2::g_trace = reinterpret_cast<uint64_t *>(buf);
+    g2::g_trace_cap = buf ? cap : 0;
+    return T >= 1 && T <= GPT2_N_CTX ? (int)g2::build_tasks(T).size() : 0;
+}
 // Synchronizes and returns (then clears) the persistent prefill's sticky error word: nonzero when a
 // launch since the last call gave up waiting (its results are void).
 extern "C" int gpt2_prefill_status(void) {

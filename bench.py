@@ -619,6 +619,77 @@ def decode_cold(B, scr, first, logits, tokens, streamed, kv_bytes, warm_ms, copi
             m.free()
 
 
+# ------------------------------------------------------------------------------ persistent prefill trace
+def prefill_trace(B, T=512, backend="int8"):
+    """The persistent prefill (csrc/prefill.hip, opt-in) beside the launch sequence at one T, and its
+    per-task trace (gpt2_tune_prefill_trace): for each task type the mean time waiting for inputs,
+    before the k-loop (the LayerNorm panel), in the k-loop (attention: the whole block), in the
+    epilogue, draining the stores and bumping the counter; the gap between a work-group's tasks."""
+    pkg, L = B.pkg, B.L
+    synth = importlib.import_module("bare_metal_gpt2_amd.synth")
+    model = pkg.Model(seeded_body())
+    if backend == "int8":
+        model.quantize()
+    ids = synth.token_ids(T, seed=1)
+    d_ids = B.dev(np.asarray(ids, np.int32))
+    scr, kv = pkg.Scratch(T), pkg.KVCache(T)
+    logits = B.empty(VOCAB * 2)
+    caps = pkg.GPT2CapsGPU()
+    caps.logits, caps.logits_all = logits.ptr, 0
+    ntask = L.gpt2_tune_prefill_trace(None, 0, T)
+    buf = B.empty(ntask * 64)
+    be = pkg.backend(backend)
+
+    def run(persistent, trace=False):
+        L.gpt2_tune_prefill_persistent(1 if persistent else 0)
+        L.gpt2_tune_prefill_trace(buf.ptr if trace else None, ntask, T)
+        L.gpt2_sync()
+        t = time.perf_counter()
+        L.gpt2_prefill_fill_cache(be, C.byref(model.gpu), C.byref(kv.kv), d_ids.ptr, T, C.byref(scr.s), C.byref(caps))
+        L.gpt2_sync()
+        pkg.check("prefill")
+        return (time.perf_counter() - t) * 1e3
+
+    try:
+        for _ in range(3):
+            run(True)
+            run(False)
+        pers = float(np.median([run(True) for _ in range(7)]))
+        seq = float(np.median([run(False) for _ in range(7)]))
+        run(True, trace=True)
+    finally:
+        L.gpt2_tune_prefill_trace(None, 0, T)
+        L.gpt2_tune_prefill_persistent(-1)
+    tr = buf.numpy(np.uint64, (ntask, 8)).astype(np.int64)
+    nrb, nqb = (T + 31) // 32, (T + 15) // 16
+    types = [0] * nrb
+    for _ in range(12):
+        types += [1] * (nrb * 36) + [2] * (nqb * 12) + [3] * (nrb * 12) + [4] * (nrb * 48) + [5] * (nrb * 24)
+    types = np.array(types)
+    ready = np.where(tr[:, 2] > 0, tr[:, 2], tr[:, 1])
+    kst = np.where(tr[:, 3] > 0, tr[:, 3], ready)
+    ken = np.where(tr[:, 4] > 0, tr[:, 4], tr[:, 5])
+    us = lambda x: x / 100.0   # s_memrealtime ticks at 100 MHz
+    phases = {"wait": us(ready - tr[:, 1]), "pre": us(kst - ready), "kloop": us(ken - kst),
+              "epilogue": us(tr[:, 5] - ken), "drain": us(tr[:, 6] - tr[:, 5]), "signal": us(tr[:, 7] - tr[:, 6])}
+    per = {}
+    for k, name in enumerate(["embed", "qkv", "attention", "attn_proj", "fc", "mlp_proj"]):
+        m = types == k
+        per[name] = {"tasks": int(m.sum()), **{p: round(float(v[m].mean()), 2) for p, v in phases.items()}}
+    gaps = []
+    for wg in np.unique(tr[:, 0]):
+        r = tr[tr[:, 0] == wg]
+        r = r[np.argsort(r[:, 1])]
+        gaps += list(us(r[1:, 1] - r[:-1, 7]))
+    span = us(tr[:, 7].max() - tr[:, 1].min())
+    scr.free()
+    kv.free()
+    model.free()
+    return {"T": T, "backend": backend, "tasks": ntask, "work_groups": int(len(np.unique(tr[:, 0]))),
+            "persistent_ms": round(pers, 4), "launch_sequence_ms": round(seq, 4), "traced_span_us": round(float(span), 1),
+            "gap_between_tasks_us": round(float(np.mean(gaps)), 2), "per_task_us": per}
+
+
 # ------------------------------------------------------------------------------ measured ceilings
 def measured_peaks(B, cus):
     """This box's ceilings, measured in the same run beside the datasheet peaks (the role of
@@ -788,6 +859,9 @@ def main():
     ap.add_argument("--decode-only", action="store_true",
                     help="only the config-5 decode leg (prefill, step at pos 512 warm and with its weights cold; "
                          "no greedy run), printed as one JSON line: the driver for the decode step's counter runs")
+    ap.add_argument("--prefill-trace", type=int, default=0, metavar="T",
+                    help="only the persistent prefill at T tokens (INT8 and fp16) beside the launch sequence, "
+                         "with its per-task trace, printed as one JSON line")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="also run one plain copy of BYTES (calibrates FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -820,6 +894,10 @@ def main():
     if args.gemv_only:
         gemv, head = bench_gemv(B, quick=True)
         print(json.dumps({"gemv_int8": gemv, "head_gemv_fp16": head}), flush=True)
+        return
+    if args.prefill_trace:
+        print(json.dumps({"prefill_trace": [prefill_trace(B, args.prefill_trace, be) for be in ("int8", "flash")]}),
+              flush=True)
         return
     if args.decode_only:
         print(json.dumps({"decode": bench_decode(B, steady_reps=32, greedy=False)}), flush=True)
