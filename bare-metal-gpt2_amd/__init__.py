@@ -89,12 +89,7 @@ class GPT2Backend(C.Structure):
         "embed", "layernorm", "matmul", "attention", "gelu", "add", "matmul_q", "gemv", "gemv_q")]
 
 
-class GPT2BenchOp(C.Structure):
-    _fields_ = [("kind", C.c_int), ("C", _vp), ("A", _vp), ("W", _vp), ("Ws", _vp), ("bias", _vp),
-                ("M", C.c_int), ("N", C.c_int), ("K", C.c_int)]
-
-
-# (name, restype, argtypes) for every symbol declared in include/*.h plus the bench/tuning hooks.
+# (name, restype, argtypes) for every symbol declared in include/*.h plus the test/tuning hooks.
 _i, _u, _sz, _d = C.c_int, C.c_uint, C.c_size_t, C.c_double
 _BE = C.POINTER(GPT2Backend)
 SIGNATURES = {
@@ -167,14 +162,6 @@ SIGNATURES = {
     "gpt2_decode_graph_destroy": (None, [_vp]),
     "gpt2_decode_graph_time": (_i, [_vp, _i, _fp]),
     # bench / tuning hooks (not part of the reference interface)
-    "gpt2_bench_ops": (_i, [C.POINTER(GPT2BenchOp), _i, _i, _i, _fp, _fp]),
-    "gpt2_bench_ops_graph": (_i, [C.POINTER(GPT2BenchOp), _i, _i, _i, _fp]),
-    "gpt2_bench_time": (_i, [_vp, _vp, _fp]),
-    "gpt2_device_info": (_i, [C.POINTER(_i), C.POINTER(_i), C.c_char_p, _i]),
-    "gpt2_bench_empty": (_i, [_i, _fp]),
-    "gpt2_bench_read": (_i, [_vp, _sz, _i, _fp]),
-    "gpt2_bench_mfma": (_i, [_i, _i, _fp]),
-    "gpt2_bench_copy": (_i, [_vp, _vp, _sz, _fp]),
     "gpt2_tune_gemm_count": (_i, []),
     "gpt2_tune_gemm_name": (C.c_char_p, [_i]),
     "gpt2_tune_gemm_pick": (_i, [_i, _i, _i]),

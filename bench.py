@@ -65,10 +65,20 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def load_harness():
+    """bench/harness.py (the binding of bench/libgpt2bench.so, the native timing loops)."""
+    here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "bench")
+    if here not in sys.path:
+        sys.path.insert(0, here)
+    return importlib.import_module("harness")
+
+
 class Bench:
     def __init__(self, pkg):
         self.pkg = pkg
         self.L = pkg.lib()
+        self.harness = load_harness()
+        self.H = self.harness.lib(pkg)    # timing loops and microbenchmarks (not the product library)
         self.keep = []
 
     def dev(self, a):
@@ -82,13 +92,13 @@ class Bench:
         return d
 
     def op(self, kind, Cb, A, W, Ws, bias, M, N, K):
-        return self.pkg.GPT2BenchOp(kind, Cb, A, W, Ws, bias, M, N, K)
+        return self.harness.GPT2BenchOp(kind, Cb, A, W, Ws, bias, M, N, K)
 
     def run_ops(self, ops, warmup, iters, per_op=False):
-        arr = (self.pkg.GPT2BenchOp * len(ops))(*ops)
+        arr = (self.harness.GPT2BenchOp * len(ops))(*ops)
         ms = C.c_float()
         per = (C.c_float * len(ops))() if per_op else None
-        rc = self.L.gpt2_bench_ops(arr, len(ops), warmup, iters, C.byref(ms),
+        rc = self.H.gpt2_bench_ops(arr, len(ops), warmup, iters, C.byref(ms),
                                    C.cast(per, C.POINTER(C.c_float)) if per_op else None)
         if rc:
             self.pkg.check("gpt2_bench_ops")
@@ -97,9 +107,9 @@ class Bench:
 
     def run_ops_graph(self, ops, warmup, iters):
         """Mean ms per round when one round is captured once as a hipGraph and replayed."""
-        arr = (self.pkg.GPT2BenchOp * len(ops))(*ops)
+        arr = (self.harness.GPT2BenchOp * len(ops))(*ops)
         ms = C.c_float()
-        rc = self.L.gpt2_bench_ops_graph(arr, len(ops), warmup, iters, C.byref(ms))
+        rc = self.H.gpt2_bench_ops_graph(arr, len(ops), warmup, iters, C.byref(ms))
         if rc:
             self.pkg.check("gpt2_bench_ops_graph")
             raise RuntimeError(f"gpt2_bench_ops_graph rc={rc}")
@@ -702,12 +712,12 @@ def measured_peaks(B, cus):
     buf = B.pkg.Dev(nbytes)
     L.gpt2_memset(buf.ptr, 1, nbytes)
     ms = C.c_float()
-    if L.gpt2_bench_read(buf.ptr, nbytes, 5, C.byref(ms)):
+    if B.H.gpt2_bench_read(buf.ptr, nbytes, 5, C.byref(ms)):
         B.pkg.check("gpt2_bench_read")
     read_gbs = nbytes / (ms.value * 1e-3) / 1e9
     buf.free()
     blocks, iters = cus, 20000
-    if L.gpt2_bench_mfma(blocks, iters, C.byref(ms)):
+    if B.H.gpt2_bench_mfma(blocks, iters, C.byref(ms)):
         B.pkg.check("gpt2_bench_mfma")
     mfma_tflops = blocks * 4.0 * iters * 4 * (32 * 32 * 16 * 2) / (ms.value * 1e-3) / 1e12
     return {"hbm_read_GBs": round(read_gbs, 1), "hbm_read_bytes": nbytes,
@@ -876,18 +886,18 @@ def main():
     import __graft_entry__
     pkg = __graft_entry__.load_package()
     L = pkg.lib()
+    B = Bench(pkg)
     cus, clk = C.c_int(), C.c_int()
     name = C.create_string_buffer(256)
-    if L.gpt2_device_info(C.byref(cus), C.byref(clk), name, 256):
+    if B.H.gpt2_device_info(C.byref(cus), C.byref(clk), name, 256):
         raise SystemExit("no HIP device visible")
-    B = Bench(pkg)
     log(f"device {name.value.decode()} CUs={cus.value} clock={clk.value / 1e3:.0f} MHz")
 
     if args.copy_probe:
         src, dst = pkg.Dev(args.copy_probe), pkg.Dev(args.copy_probe)
         L.gpt2_memset(src.ptr, 1, args.copy_probe)
         ms = C.c_float()
-        L.gpt2_bench_copy(dst.ptr, src.ptr, args.copy_probe, C.byref(ms))
+        B.H.gpt2_bench_copy(dst.ptr, src.ptr, args.copy_probe, C.byref(ms))
         log(f"copy probe: {args.copy_probe} B in {ms.value * 1e3:.1f} us")
         src.free()
         dst.free()

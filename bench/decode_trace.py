@@ -5,7 +5,7 @@ leg), creates a persistent decode graph with the profiling hook `gpt2_tune_decod
 it `--reps` times at position 512 and prints, per layer, when each phase's input arrived and when its
 work-groups finished (s_memrealtime, 100 MHz), plus the layer-1 sub-phase marks.
 
-    python bare-metal-gpt2_amd/decode_trace.py [--reps 20] [--backend int8]
+    python bench/decode_trace.py [--reps 20] [--backend int8]
 
 Phases per layer l: 4l attention work-groups (0..47: LN1, q/k/v, attention), 4l+1 proj, 4l+2 fc,
 4l+3 mlp-proj (GEMV work-groups 48..239).  "wait" is the median arrival of a phase's input minus the

@@ -1,6 +1,6 @@
 """Times the prefill forward of a seeded GPT-2-124M-shaped body (the config-5 prefill).
 
-    python bare-metal-gpt2_amd/prefill_bench.py [--tokens 512] [--reps 8] [--backend int8] [--unfused]
+    python bench/prefill_bench.py [--tokens 512] [--reps 8] [--backend int8] [--unfused]
 
 Each repetition is one `gpt2_prefill_fill_cache` call (embed, 12 layers, final LayerNorm, the last
 row's logits, the K/V cache fill), host-timed around a device sync; the first call is reported
