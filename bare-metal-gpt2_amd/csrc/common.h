@@ -98,6 +98,41 @@ __device__ __forceinline__ uint16_t f2h(float f) {
     return __builtin_bit_cast(uint16_t, (f16)f);   // v_cvt_f16_f32: round to nearest even
 }
 
+// LayerNorm of one 768-wide row held by one wave, lane l holding elements 256 i + 4 l + c (i < 3,
+// c < 4): the mean, then the mean squared deviation from it, eps inside the square root
+// (cuda/kernels_naive.cu:26-41), in fp32.  Every kernel that normalizes rows (the LayerNorm kernel,
+// the GEMMs that normalize their own A panel) goes through this function, so they agree bit for
+// bit: the fp32 operations are written out (explicit fma) and each output is pinned in fp32 before
+// its conversion, so no kernel can fold the conversion into the fma (v_fma_mix: one rounding
+// instead of two) where another does not.
+__device__ __forceinline__ void ln_row768(const f16x4 (&x)[3], const f16x4 (&g)[3], const f16x4 (&b)[3],
+                                          f16x4 (&o)[3]) {
+    float v[12];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[4 * i + c] = (float)x[i][c];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 12; ++i) s += v[i];
+    const float mean = wave_sum(s) / (float)GPT2_N_EMBD;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+        const float d = v[i] - mean;
+        q = __builtin_fmaf(d, d, q);
+    }
+    const float rstd = 1.0f / sqrtf(wave_sum(q) / (float)GPT2_N_EMBD + GPT2_LN_EPS);
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            float y = __builtin_fmaf((v[4 * i + c] - mean) * rstd, (float)g[i][c], (float)b[i][c]);
+            asm volatile("" : "+v"(y));
+            o[i][c] = (f16)y;
+        }
+}
+
 // gelu_new, the tanh form (model/config.h:41-42): 0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))).
 // The decode kernels (fused GEMV epilogue, persistent step) use this form.
 __device__ __forceinline__ float gelu_tanh(float v) {

@@ -19,6 +19,8 @@ void gemv(uint16_t *C, const uint16_t *x, const void *W, const float *Ws, const 
 void embed_one(uint16_t *x, const uint16_t *wte, const uint16_t *wpe, StepArg st);
 bool gemm_fused(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const uint16_t *bias, int M, int N,
                 int K, bool qw, int epi, const uint16_t *resid);
+bool gemm_ln(uint16_t *C, const uint16_t *X, const uint16_t *ln_g, const uint16_t *ln_b, const void *W,
+             const float *Ws, const uint16_t *bias, int M, int N, int K, bool qw, int epi, int cfg);
 void attention_prefill(uint16_t *att, const uint16_t *qkv, int T, uint16_t *Kc, uint16_t *Vc, int maxT);
 void kv_append(uint16_t *K, uint16_t *V, const uint16_t *qkv, StepArg st, int maxT);
 void attn_decode(uint16_t *att, const uint16_t *qkv, const uint16_t *K, const uint16_t *V, int maxT, StepArg st,
@@ -238,6 +240,22 @@ static void matmul_site(const GPT2Backend *be, bool fused, gpt2_half *C, const g
     }
 }
 
+// LayerNorm(X) followed by a matmul site (QKV: no epilogue; fc: gelu): one LayerNorm-panel GEMM
+// launch when a panel config is forced (gpt2_tune_gemm_ln_force; off by default, slower than the two
+// launches) and the fused prefill may use it (ln_fuse also requires this library's LayerNorm, whose
+// arithmetic the panel repeats bit for bit), else the backend's LayerNorm into lnbuf, then the site.
+static void ln_matmul_site(const GPT2Backend *be, bool fused, bool ln_fuse, gpt2_half *C, const gpt2_half *X,
+                           const gpt2_half *ln_g, const gpt2_half *ln_b, gpt2_half *lnbuf, const gpt2_half *Wh,
+                           const GPT2QW *Wq, const gpt2_half *bias, int M, int N, int K, int epi) {
+    const bool q = be->matmul_q && Wq && Wq->q;
+    if (ln_fuse && gemm_ln(C, X, ln_g, ln_b, q ? (const void *)Wq->q : (const void *)Wh, q ? Wq->s : nullptr, bias, M,
+                           N, K, q, epi, -1))
+        return;
+    be->layernorm(lnbuf, X, ln_g, ln_b, M, K);
+    if (epi == EPI_NONE) gpt2_matmul_dispatch(be, C, lnbuf, Wh, Wq, bias, M, N, K);
+    else matmul_site(be, fused, C, lnbuf, Wh, Wq, bias, M, N, K, epi, nullptr);
+}
+
 // persistent: the trunk may run as the persistent kernel (it allocates its arena on first use, so
 // the no-allocation entry point runs the launch sequence instead).
 static void forward_impl(const GPT2Backend *be, const GPT2WeightsGPU *w, const int *d_ids, int T, GPT2ScratchGPU *s,
@@ -282,13 +300,14 @@ static void forward_impl(const GPT2Backend *be, const GPT2WeightsGPU *w, const i
     }
     // the attention launch fills the cache itself when it is this library's prefill attention
     const bool attn_kv = fused && be->attention == gpt2_attention_flash && kv && kv->data;
+    const bool ln_fuse = fused && be->layernorm == gpt2_layernorm;
     be->embed(s->x, w->wte, w->wpe, d_ids, T, E);
     if (caps && caps->embed) capcpy(caps->embed, s->x, (size_t)T * E);
     for (int L = 0; L < GPT2_N_LAYER; ++L) {
         const GPT2LayerGPU *ly = &w->layers[L];
         const GPT2QLayerGPU *qy = qw ? &qw->layers[L] : nullptr;
-        be->layernorm(s->ln, s->x, ly->ln1_g, ly->ln1_b, T, E);
-        gpt2_matmul_dispatch(be, s->qkv, s->ln, ly->qkv_w, qy ? &qy->qkv_w : nullptr, ly->qkv_b, T, Q, E);
+        ln_matmul_site(be, fused, ln_fuse, s->qkv, s->x, ly->ln1_g, ly->ln1_b, s->ln, ly->qkv_w,
+                       qy ? &qy->qkv_w : nullptr, ly->qkv_b, T, Q, E, EPI_NONE);
         if (attn_kv && L < kv->nLayer) {
             attention_prefill(s->att, s->qkv, T, gpt2_kv_K(kv, L), gpt2_kv_V(kv, L), kv->maxT);
         } else {
@@ -297,8 +316,8 @@ static void forward_impl(const GPT2Backend *be, const GPT2WeightsGPU *w, const i
         }
         matmul_site(be, fused, s->x, s->att, ly->attn_proj_w, qy ? &qy->attn_proj_w : nullptr, ly->attn_proj_b, T, E, E,
                     EPI_RESID, s->ao);
-        be->layernorm(s->ln, s->x, ly->ln2_g, ly->ln2_b, T, E);
-        matmul_site(be, fused, s->fc, s->ln, ly->fc_w, qy ? &qy->fc_w : nullptr, ly->fc_b, T, F, E, EPI_GELU, nullptr);
+        ln_matmul_site(be, fused, ln_fuse, s->fc, s->x, ly->ln2_g, ly->ln2_b, s->ln, ly->fc_w,
+                       qy ? &qy->fc_w : nullptr, ly->fc_b, T, F, E, EPI_GELU);
         matmul_site(be, fused, s->x, s->fc, ly->proj_w, qy ? &qy->proj_w : nullptr, ly->proj_b, T, E, F, EPI_RESID,
                     s->ff);
         if (caps && caps->blocks) capcpy(caps->blocks + (size_t)L * T * E, s->x, (size_t)T * E);

@@ -267,28 +267,34 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(uint16_t *__restrict__ C, con
 // U > 1 covers U consecutive k-tiles per barrier: their fragments are read back to back (one LDS
 // round trip) and then multiplied, and U tiles are refilled at a time (S % U == 0, S >= 2U).
 // EPI: the elementwise op fused into the epilogue (EPI_GELU; EPI_RESID adds resid, which may be C).
-template <int BN, int BM, int WN, int WM, int S, bool QW, int KS = 1, int U = 1, int EPI = EPI_NONE>
-__global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
-                                                         const void *__restrict__ Wv, const float *__restrict__ Ws,
-                                                         const uint16_t *__restrict__ bias, int M, int N, int K,
-                                                         int tiles_m, int ntiles, int vec_store,
-                                                         const uint16_t *resid) {
+// LNP (k_gemm_dl_ln): A is the LayerNorm of X[m0 .. m0+BM) (K = 768, gamma ln_g, beta ln_b), built
+// once per work-group into an LDS panel that holds all of the tile's A; the ring then carries W only.
+template <int BN, int BM, int WN, int WM, int S, bool QW, int KS, int U, int EPI, bool LNP>
+__device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
+                                        const void *__restrict__ Wv, const float *__restrict__ Ws,
+                                        const uint16_t *__restrict__ bias, int M, int N, int K, int tiles_m,
+                                        int ntiles, int vec_store, const uint16_t *resid,
+                                        const uint16_t *__restrict__ ln_g, const uint16_t *__restrict__ ln_b) {
 #if defined(__HIP_DEVICE_COMPILE__)   // LDS address-space pointers exist only in the device pass
     constexpr int NW = WN * WM;
     constexpr int BK = 64;
     constexpr int A_BYTES = BM * BK * 2;        // fp16 A tile: rows of 128 B (8 chunks)
+    constexpr int RA = LNP ? 0 : A_BYTES;       // A bytes per ring stage (the LN panel holds all of A)
     constexpr int W_ROWB = QW ? BK : BK * 2;    // W tile rows: 64 B int8 (4 chunks) or 128 B fp16
     constexpr int W_BYTES = BN * W_ROWB;
-    constexpr int STAGE = A_BYTES + W_BYTES;
-    constexpr int A_INS = A_BYTES / 1024, W_INS = W_BYTES / 1024;
+    constexpr int STAGE = RA + W_BYTES;
+    constexpr int PANEL = LNP ? BM * GPT2_N_EMBD * 2 : 0;
+    constexpr int A_INS = RA / 1024, W_INS = W_BYTES / 1024;
     static_assert(A_BYTES % 1024 == 0 && W_BYTES % 1024 == 0, "1 KB load granules");
+    static_assert(!LNP || (KS == 1 && EPI != EPI_RESID), "the LN panel form has one k group, no residual");
     constexpr int TOT = A_INS + W_INS, LO = TOT / NW, REM = TOT % NW, LMAX = LO + (REM ? 1 : 0);
     constexpr int WTN = BN / WN, WTM = BM / WM, TN = WTN / 16, TM = WTM / 16;
     static_assert(TN * 16 == WTN && TM * 16 == WTM, "wave tile is whole 16x16 blocks");
     static_assert(S >= 2 && (S - 2) * LMAX < 64, "stages");
     static_assert(U >= 1 && S % U == 0 && S >= 2 * U, "k-tiles per barrier");
 
-    __shared__ __attribute__((aligned(1024))) char smem_all[KS * S * STAGE];
+    __shared__ __attribute__((aligned(1024))) char smem_all[KS * S * STAGE + PANEL];
+    char *const panel = smem_all + KS * S * STAGE;   // LNP: 12 k-tile blocks of A, as a ring stage lays them out
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -319,7 +325,7 @@ __global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restri
             else { row = 8 * qw + (lane >> 3); c = (lane & 7) ^ (row & 7); }
             const int n = min(n0 + row, N - 1);
             gsrc[j] = reinterpret_cast<const char *>(Wv) + (size_t)n * K * welt + c * 16;
-            ldst[j] = A_BYTES + qw * 1024;
+            ldst[j] = RA + qw * 1024;
             kstep[j] = BK * (int)welt;
         }
     }
@@ -357,22 +363,23 @@ __global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restri
     };
     auto load_frags = [&](int kt, Frag &F) {
         const char *st = smem + (kt % S) * STAGE;
+        const char *sa = LNP ? panel + kt * A_BYTES : st;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const int c = ks * 4 + lgrp;
 #pragma unroll
             for (int b = 0; b < TM; ++b) {
                 const int r = wm0 + b * 16 + lrow;
-                F.fa[ks][b] = *reinterpret_cast<const f16x8 *>(st + r * 128 + ((c ^ (r & 7)) << 4));
+                F.fa[ks][b] = *reinterpret_cast<const f16x8 *>(sa + r * 128 + ((c ^ (r & 7)) << 4));
             }
 #pragma unroll
             for (int a = 0; a < TN; ++a) {
                 const int r = wn0 + a * 16 + lrow;
                 if constexpr (QW) {
                     const int cq = (ks * 2 + (lgrp >> 1)) ^ ((r >> 2) & 3);
-                    F.wq[ks][a] = *reinterpret_cast<const uint2 *>(st + A_BYTES + r * 64 + (cq << 4) + ((lgrp & 1) << 3));
+                    F.wq[ks][a] = *reinterpret_cast<const uint2 *>(st + RA + r * 64 + (cq << 4) + ((lgrp & 1) << 3));
                 } else {
-                    F.fw[ks][a] = *reinterpret_cast<const f16x8 *>(st + A_BYTES + r * 128 + ((c ^ (r & 7)) << 4));
+                    F.fw[ks][a] = *reinterpret_cast<const f16x8 *>(st + RA + r * 128 + ((c ^ (r & 7)) << 4));
                 }
             }
         }
@@ -421,9 +428,44 @@ __global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restri
             }
     }
 
+    // LNP: the tile's rows of X and gamma/beta are loaded first, the ring's first W tiles go out right
+    // behind them, and the LayerNorm runs while those are in flight.  Wave w normalizes rows w,
+    // w + NW, ...; where NW does not divide BM a wave repeats row BM-1 (the same bits to the same
+    // LDS bytes).  Rows past M normalize row M-1 (never stored).  The first barrier of the k-loop
+    // orders the panel writes before any fragment read.
+    constexpr int RPW = LNP ? (BM + NW - 1) / NW : 1;
+    f16x4 lx[RPW][3], lg[3], lb[3];
+    if constexpr (LNP) {
+        const int lane4 = 4 * lane;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            lg[i] = *reinterpret_cast<const f16x4 *>(ln_g + 256 * i + lane4);
+            lb[i] = *reinterpret_cast<const f16x4 *>(ln_b + 256 * i + lane4);
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int row = min(wave + NW * r, BM - 1);
+            const uint16_t *xr = A + (size_t)min(m0 + row, M - 1) * GPT2_N_EMBD;
+#pragma unroll
+            for (int i = 0; i < 3; ++i) lx[r][i] = *reinterpret_cast<const f16x4 *>(xr + 256 * i + lane4);
+        }
+    }
     // Prologue: tiles 0 .. S-U-1 in flight (the config table requires nk >= S - U, nk % U == 0).
 #pragma unroll
     for (int s = 0; s < S - U; ++s) issue(s);
+    if constexpr (LNP) {
+        const int chunk = (lane & 15) >> 1;
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int row = min(wave + NW * r, BM - 1);
+            f16x4 o[3];
+            ln_row768(lx[r], lg, lb, o);
+#pragma unroll
+            for (int i = 0; i < 3; ++i)   // elements 256 i + 4 lane .. +3: k-tile 4 i + lane / 16
+                *reinterpret_cast<f16x4 *>(panel + (4 * i + (lane >> 4)) * A_BYTES + row * 128 +
+                                           ((chunk ^ (row & 7)) << 4) + (lane & 1) * 8) = o[i];
+        }
+    }
     int kt = 0;
     for (; kt + S - U < nk; kt += U) {
         wait_for(S - 2 * U);   // tiles kt .. kt+U-1 have landed (this wave's part; the barrier: all)
@@ -541,6 +583,33 @@ __global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restri
         }
     }
 #endif
+}
+
+template <int BN, int BM, int WN, int WM, int S, bool QW, int KS = 1, int U = 1, int EPI = EPI_NONE>
+__global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
+                                                         const void *__restrict__ Wv, const float *__restrict__ Ws,
+                                                         const uint16_t *__restrict__ bias, int M, int N, int K,
+                                                         int tiles_m, int ntiles, int vec_store,
+                                                         const uint16_t *resid) {
+    gemm_dl<BN, BM, WN, WM, S, QW, KS, U, EPI, false>(C, A, Wv, Ws, bias, M, N, K, tiles_m, ntiles, vec_store, resid,
+                                                      nullptr, nullptr);
+}
+
+// C = LayerNorm(X; ln_g, ln_b) . W^T (+ bias) (then gelu for EPI_GELU), K = 768: the prefill's
+// LN1 -> QKV and LN2 -> fc without the LayerNorm launch and its round trip through memory.  Each
+// work-group normalizes its BM rows of X itself (the rows are recomputed by every work-group of the
+// same rows: N / BN times the LayerNorm's arithmetic, its reads served by L2), with the LayerNorm
+// kernel's arithmetic (ln_row768), so C is bit-identical to the LayerNorm kernel followed by the
+// plain GEMM on any one-k-group config.
+template <int BN, int BM, int WN, int WM, int S, bool QW, int U, int EPI>
+__global__ __launch_bounds__(WN *WM * 64) void k_gemm_dl_ln(uint16_t *__restrict__ C, const uint16_t *__restrict__ X,
+                                                       const void *__restrict__ Wv, const float *__restrict__ Ws,
+                                                       const uint16_t *__restrict__ bias, int M, int N, int K,
+                                                       int tiles_m, int ntiles, int vec_store,
+                                                       const uint16_t *__restrict__ ln_g,
+                                                       const uint16_t *__restrict__ ln_b) {
+    gemm_dl<BN, BM, WN, WM, S, QW, 1, U, EPI, true>(C, X, Wv, Ws, bias, M, N, K, tiles_m, ntiles, vec_store, nullptr,
+                                                    ln_g, ln_b);
 }
 
 // Any shape, any alignment: 16x16 outputs per work-group, k staged through LDS as fp32.
@@ -684,6 +753,26 @@ static const GemmCfg kGuardCfgs[] = {
     G2_GCFG(64, 32, 2, 2),
 };
 
+// LayerNorm-panel GEMMs (k_gemm_dl_ln): K = 768, BM = 32, one k group.
+typedef void (*GemmLnFn)(uint16_t *, const uint16_t *, const void *, const float *, const uint16_t *, int, int, int,
+                         int, int, int, const uint16_t *, const uint16_t *);
+struct GemmLnCfg {
+    int bn, bm, threads;
+    GemmLnFn fn[2][2];   // [int8][EPI_NONE, EPI_GELU]
+    const char *name;
+};
+#define G2_LNCFG(BN, BM, WN, WM, S, U)                                                                         \
+    {BN, BM, 64 * WN * WM,                                                                                     \
+     {{k_gemm_dl_ln<BN, BM, WN, WM, S, false, U, EPI_NONE>, k_gemm_dl_ln<BN, BM, WN, WM, S, false, U, EPI_GELU>}, \
+      {k_gemm_dl_ln<BN, BM, WN, WM, S, true, U, EPI_NONE>, k_gemm_dl_ln<BN, BM, WN, WM, S, true, U, EPI_GELU>}},  \
+     "ln_bn" #BN "_bm" #BM "_w" #WN "x" #WM "_s" #S "_u" #U}
+static const GemmLnCfg kLnCfgs[] = {
+    G2_LNCFG(64, 32, 2, 2, 4, 2),   // 0: 4 waves, wave tile 32x16
+    G2_LNCFG(96, 32, 6, 1, 4, 2),   // 1: 6 waves, wave tile 16x32
+    G2_LNCFG(96, 32, 3, 1, 4, 2),   // 2: 3 waves, wave tile 32x32
+};
+static const int kNumLnCfgs = (int)(sizeof(kLnCfgs) / sizeof(kLnCfgs[0]));
+
 static int g_force_cfg = -2;  // -2: not read yet; -1: table
 
 static bool cfg_fits(int c, int K) { return K % kCfgs[c].kmul == 0 && K >= kCfgs[c].kmin; }
@@ -813,6 +902,33 @@ bool gemm_fused(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, 
     return true;
 }
 
+// The prefill's LayerNorm-panel fusion is off unless a config is forced (gpt2_tune_gemm_ln_force):
+// measured on MI355X (bench/prefill_bench.py --ln-cfg) the whole P=512 INT8 prefill takes 0.754 ms
+// with the best config against 0.608 ms with the LayerNorm launch and the plain GEMM (T=1024: 1.16
+// against 0.91 ms; T=128: no faster).  Every work-group of a 32-row block normalizes the same 32 rows
+// before its first MFMA (24 to 48 work-groups per row block), each wave reducing 6 to 11 rows in
+// sequence, and the 48 KB panel halves the work-groups resident per CU.
+static int g_ln_cfg = -1;   // >= 0: the prefill's QKV and fc run that config; -1: off
+
+// C = LayerNorm(X; ln_g, ln_b) . W^T (+ bias), then gelu for EPI_GELU, in one launch (K = 768).
+// cfg < 0 takes the forced config, if any.  Returns false (nothing launched) when no LayerNorm-panel kernel
+// covers the call: the caller then runs the LayerNorm kernel and the GEMM.
+bool gemm_ln(uint16_t *C, const uint16_t *X, const uint16_t *ln_g, const uint16_t *ln_b, const void *W,
+             const float *Ws, const uint16_t *bias, int M, int N, int K, bool qw, int epi, int cfg) {
+    if (M <= 1 || N <= 0 || K != GPT2_N_EMBD || !mfma_ok(X, W, K, qw)) return false;
+    if (!ln_g || !ln_b || (((uintptr_t)ln_g | (uintptr_t)ln_b) & 7u)) return false;
+    if (epi != EPI_NONE && epi != EPI_GELU) return false;
+    const int c = cfg >= 0 ? (cfg < kNumLnCfgs ? cfg : -1) : g_ln_cfg;
+    if (c < 0) return false;
+    const GemmLnCfg &g = kLnCfgs[c];
+    const int tiles_m = cdiv(M, g.bm), ntiles = tiles_m * cdiv(N, g.bn);
+    const int vec = (N % 4 == 0) && (((uintptr_t)C & 7u) == 0);
+    hipLaunchKernelGGL(g.fn[qw ? 1 : 0][epi == EPI_GELU ? 1 : 0], dim3(ntiles), dim3(g.threads), 0, stream(), C, X, W,
+                       Ws, bias, M, N, K, tiles_m, ntiles, vec, ln_g, ln_b);
+    check_launch(qw ? "k_gemm_dl_ln<int8>" : "k_gemm_dl_ln<fp16>");
+    return true;
+}
+
 }  // namespace g2
 
 using namespace g2;
@@ -859,4 +975,15 @@ extern "C" int gpt2_tune_gemm_fused(gpt2_half *C, const gpt2_half *A, const void
                                     const gpt2_half *bias, int M, int N, int K, int epi, const gpt2_half *resid) {
     if (gemm_args("gpt2_tune_gemm_fused", C, A, W, M, N, K)) return 0;
     return gemm_fused(C, A, W, Ws, bias, M, N, K, Ws != nullptr, epi, resid) ? 1 : 0;
+}
+// The LayerNorm-panel GEMMs: C = LayerNorm(X; g, b) . W^T (+ bias), gelu after for epi 1; cfg -1
+// takes the forced config.  Returns 1 when a kernel ran, 0 when none covers the call.
+extern "C" int gpt2_tune_gemm_ln_count(void) { return kNumLnCfgs; }
+extern "C" const char *gpt2_tune_gemm_ln_name(int cfg) { return cfg >= 0 && cfg < kNumLnCfgs ? kLnCfgs[cfg].name : "?"; }
+// Force one LayerNorm-panel config for the prefill's QKV and fc GEMMs (-1: off, the default).
+extern "C" void gpt2_tune_gemm_ln_force(int cfg) { g_ln_cfg = (cfg >= 0 && cfg < kNumLnCfgs) ? cfg : -1; }
+extern "C" int gpt2_tune_gemm_ln(int cfg, gpt2_half *C, const gpt2_half *X, const gpt2_half *g, const gpt2_half *b,
+                                 const void *W, const float *Ws, const gpt2_half *bias, int M, int N, int K, int epi) {
+    if (gemm_args("gpt2_tune_gemm_ln", C, X, W, M, N, K)) return 0;
+    return gemm_ln(C, X, g, b, W, Ws, bias, M, N, K, Ws != nullptr, epi, cfg) ? 1 : 0;
 }

@@ -51,37 +51,19 @@ __global__ __launch_bounds__(256) void k_layernorm(uint16_t *__restrict__ out, c
     const uint16_t *xr = x + (size_t)row * E;
     uint16_t *o = out + (size_t)row * E;
     if constexpr (VEC768) {
-        // 768 = 3 x (64 lanes x 4 halves): keep the row in registers between the passes; gamma and
-        // beta are loaded with the row, so their latency hides behind the two reductions
-        float v[12];
-        f16x4 gg[3], bb[3];
+        // E = 768 = 3 x (64 lanes x 4 halves): the row stays in registers between the passes; gamma
+        // and beta are loaded with the row, so their latency hides behind the two reductions.  The
+        // arithmetic is ln_row768's, shared with the GEMMs that normalize their own A panel.
+        f16x4 h[3], gg[3], bb[3], r[3];
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
-            const f16x4 h = *reinterpret_cast<const f16x4 *>(xr + 256 * i + 4 * lane);
+            h[i] = *reinterpret_cast<const f16x4 *>(xr + 256 * i + 4 * lane);
             gg[i] = *reinterpret_cast<const f16x4 *>(g + 256 * i + 4 * lane);
             bb[i] = *reinterpret_cast<const f16x4 *>(b + 256 * i + 4 * lane);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) v[4 * i + c] = (float)h[c];
         }
-        float s = 0.f;
+        ln_row768(h, gg, bb, r);
 #pragma unroll
-        for (int i = 0; i < 12; ++i) s += v[i];
-        const float mean = wave_sum(s) / E;
-        float q = 0.f;
-#pragma unroll
-        for (int i = 0; i < 12; ++i) {
-            const float d = v[i] - mean;
-            q += d * d;
-        }
-        const float rstd = 1.0f / sqrtf(wave_sum(q) / E + GPT2_LN_EPS);
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            const int e0 = 256 * i + 4 * lane;
-            f16x4 r;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) r[c] = (f16)((v[4 * i + c] - mean) * rstd * (float)gg[i][c] + (float)bb[i][c]);
-            *reinterpret_cast<f16x4 *>(o + e0) = r;
-        }
+        for (int i = 0; i < 3; ++i) *reinterpret_cast<f16x4 *>(o + 256 * i + 4 * lane) = r[i];
         return;
     } else {
     float s = 0.f;

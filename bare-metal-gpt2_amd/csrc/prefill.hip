@@ -124,8 +124,7 @@ struct TileGeo {
 };
 
 // LayerNorm of rows m0 .. m0+31 of X (row stride 768) into the LDS panel: wave w normalizes rows
-// 8w .. 8w+7, lane l holding elements 256 i + 4 l + c as the LayerNorm kernel does (same sums in
-// the same order).  The panel is 12 k-tile blocks of 32 rows x 128 B, each laid out as a ring stage's
+// 8w .. 8w+7 with ln_row768, the LayerNorm kernel's own arithmetic (bit-identical rows).  The panel is 12 k-tile blocks of 32 rows x 128 B, each laid out as a ring stage's
 // A tile (16-byte chunk c of row r at (c ^ (r & 7)) * 16).
 __device__ __forceinline__ void ln_panel(char *panel, const uint16_t *X, const uint16_t *g, const uint16_t *b, int m0,
                                          int T) {
@@ -144,39 +143,23 @@ __device__ __forceinline__ void ln_panel(char *panel, const uint16_t *X, const u
     }
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-        float v[12];
-#pragma unroll
-        for (int i = 0; i < 3; ++i)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) v[4 * i + c] = (float)xv[r][i][c];
-        float s = 0.f;
-#pragma unroll
-        for (int i = 0; i < 12; ++i) s += v[i];
-        const float mean = wave_sum(s) / GPT2_N_EMBD;
-        float q = 0.f;
-#pragma unroll
-        for (int i = 0; i < 12; ++i) {
-            const float d = v[i] - mean;
-            q += d * d;
-        }
-        const float rstd = 1.0f / sqrtf(wave_sum(q) / GPT2_N_EMBD + GPT2_LN_EPS);
+        f16x4 o[3];
+        ln_row768(xv[r], gg, bb, o);
         const int row = 8 * wave + r;
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
-            f16x4 o;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) o[c] = (f16)((v[4 * i + c] - mean) * rstd * (float)gg[i][c] + (float)bb[i][c]);
             const int kt = 4 * i + (lane >> 4), chunk = (lane & 15) >> 1;
-            *reinterpret_cast<f16x4 *>(panel + kt * 4096 + row * 128 + ((chunk ^ (row & 7)) << 4) + (lane & 1) * 8) = o;
+            *reinterpret_cast<f16x4 *>(panel + kt * 4096 + row * 128 + ((chunk ^ (row & 7)) << 4) + (lane & 1) * 8) = o[i];
         }
     }
 }
 
 // deps(): the task's dependency wait (thread 0 polls; every thread returns its outcome).
 template <int BN, bool PANEL, bool QW, int EPI, class Deps>
-__device__ bool pf_gemm(char *lds, Deps deps, const uint16_t *A, int K, const uint16_t *ln_g,
-                        const uint16_t *ln_b, const void *Wv, const float *Ws, const uint16_t *bias,
-                        const uint16_t *resid, uint16_t *C, int N, int m0, int n0, int T, uint64_t *tr) {
+__device__ bool pf_gemm(char *lds, Deps deps, const uint16_t *__restrict__ A, int K, const uint16_t *__restrict__ ln_g,
+                        const uint16_t *__restrict__ ln_b, const void *__restrict__ Wv, const float *__restrict__ Ws,
+                        const uint16_t *__restrict__ bias, const uint16_t *__restrict__ resid, uint16_t *__restrict__ C,
+                        int N, int m0, int n0, int T, uint64_t *tr) {
     using G = TileGeo<BN, PANEL, QW>;
     constexpr int S = G::S, BK = G::BK, LMAX = G::LMAX, LO = G::LO, REM = G::REM, TM = G::TM;
     const int tid = threadIdx.x, lane = tid & 63;

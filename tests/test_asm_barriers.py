@@ -8,20 +8,11 @@ end straight back to the barrier before the next task word, re-reading the old o
 waited -- the work-group re-ran its first task forever.  The kernels now branch only on wave-uniform
 values around barriers; this test compiles them (hipcc -S, the flags of csrc/Makefile) and reads the
 loop structure from the compiler's block comments.  CPU only: it needs hipcc, not a GPU."""
-import os
 import re
-import shutil
-import subprocess
 
 import pytest
 
-HERE = os.path.dirname(os.path.abspath(__file__))
-ROOT = os.path.dirname(HERE)
-CSRC = os.path.join(ROOT, "bare-metal-gpt2_amd", "csrc")
-HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-FLAGS = ["-O3", "-std=c++17", "--offload-arch=gfx950", "-I" + os.path.join(ROOT, "include"),
-         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S"]
-EXTRA = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}   # as in csrc/Makefile
+from asm_util import device_asm
 
 
 def blocks(lines):
@@ -95,13 +86,7 @@ def test_scanner_flags_the_known_pattern():
 
 
 @pytest.mark.parametrize("src", ["prefill.hip", "decode.hip"])
-def test_persistent_kernels_have_uniform_loops_around_barriers(src, tmp_path):
-    if not shutil.which(HIPCC) and not os.path.exists(HIPCC):
-        pytest.skip("hipcc not available")
-    out = tmp_path / (src + ".s")
-    r = subprocess.run([HIPCC, *FLAGS, *EXTRA.get(src, []), os.path.join(CSRC, src), "-o", str(out)],
-                       capture_output=True, text=True, timeout=600)
-    assert r.returncode == 0, r.stderr[-2000:]
-    asm = out.read_text()
+def test_persistent_kernels_have_uniform_loops_around_barriers(src):
+    asm = device_asm(src)
     assert "s_barrier" in asm and "Loop Header" in asm
     assert hazardous_loops(asm) == []

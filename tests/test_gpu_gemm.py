@@ -315,3 +315,60 @@ def test_fused_epilogues(pkg, L, kind, M, N, K):
             assert ran == 1, (kind, M, N, K, epi)
             got = oracle.f16_to_f32(dC.numpy(np.uint16, (M, N)))
             tol_check(got, want)
+
+
+@pytest.mark.parametrize("kind", ["fp16", "int8"])
+@pytest.mark.parametrize("M,N", [(512, 2304), (512, 3072), (200, 2304), (33, 3072), (1024, 2304), (2, 3072)])
+def test_ln_panel_gemm(pkg, L, kind, M, N):
+    """The LayerNorm-panel GEMMs (the prefill's LN1 -> QKV and LN2 -> fc in one launch, K = 768), every
+    config, no epilogue and gelu: (a) bit for bit against gpt2_layernorm followed by the same GEMM on a
+    one-k-group tile config (35) and gpt2_gelu -- the identity the fused prefill relies on; (b) against
+    the oracle's layernorm, matmul and gelu (cpu/forward_cpu.c:35-50,52-69) on the same fp16 values, bar
+    as above.  M = 200, 33 and 2 leave a partial 32-row block (rows past M normalize row M-1, unstored)."""
+    K = 768
+    rng = np.random.default_rng(M * 13 + N)
+    X = oracle.fp16_view(rng.standard_normal((M, K), dtype=np.float32) +
+                         rng.standard_normal((M, 1), dtype=np.float32) * np.float32(2.0))
+    g = oracle.fp16_view(1.0 + rng.standard_normal(K, dtype=np.float32) * np.float32(0.2))
+    bl = f16v(rng, K, 0.1)
+    b = f16v(rng, N, 0.01)
+    if kind == "int8":
+        q, s, _ = oracle.quantize_fp16_view(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+        Wd = oracle.dequantize(q, s)
+        dW, ds = pkg.Dev.from_numpy(q), pkg.Dev.from_numpy(s)
+    else:
+        Wd = f16v(rng, (N, K), 0.02)
+        dW, ds = dev16(pkg, Wd), None
+    sp = ds.ptr if ds is not None else None
+    dX, dg, dbl, db = dev16(pkg, X), dev16(pkg, g), dev16(pkg, bl), dev16(pkg, b)
+    dLN, dRef = pkg.Dev(M * K * 2), pkg.Dev(M * N * 2)
+    L.gpt2_layernorm(dLN.ptr, dX.ptr, dg.ptr, dbl.ptr, M, K)
+    assert L.gpt2_tune_gemm_fits(35, K)
+    L.gpt2_tune_gemm_run(35, dRef.ptr, dLN.ptr, dW.ptr, sp, db.ptr, M, N, K)
+    L.gpt2_sync()
+    pkg.check("layernorm + gemm")
+    plain = dRef.numpy(np.uint16, (M, N))
+    L.gpt2_gelu(dRef.ptr, M * N)
+    L.gpt2_sync()
+    gelu = dRef.numpy(np.uint16, (M, N))
+
+    ln = oracle.fp16_view(oracle.layernorm(X, g, bl))
+    base = oracle.fp16_view(oracle.matmul(ln, Wd, b))
+    want = {0: base, 1: oracle.fp16_view(oracle.gelu(base))}
+    exact = {0: plain, 1: gelu}
+    dC = pkg.Dev(M * N * 2)
+    for cfg in range(L.gpt2_tune_gemm_ln_count()):
+        name = L.gpt2_tune_gemm_ln_name(cfg).decode()
+        for epi in (0, 1):
+            L.gpt2_memset(dC.ptr, 0xFF, M * N * 2)
+            ran = L.gpt2_tune_gemm_ln(cfg, dC.ptr, dX.ptr, dg.ptr, dbl.ptr, dW.ptr, sp, db.ptr, M, N, K, epi)
+            L.gpt2_sync()
+            pkg.check("ln gemm " + name)
+            assert ran == 1, (name, epi)
+            got = dC.numpy(np.uint16, (M, N))
+            bad = np.flatnonzero(got != exact[epi])
+            assert bad.size == 0, f"{name} epi={epi}: {bad.size} elements differ from layernorm + gemm, first at {bad[0]}"
+            tol_check(oracle.f16_to_f32(got), want[epi])
+    # shapes the LayerNorm panel does not take: the caller falls back to the two launches
+    assert L.gpt2_tune_gemm_ln(0, dC.ptr, dX.ptr, dg.ptr, dbl.ptr, dW.ptr, sp, db.ptr, M, N // 2, K // 2, 0) == 0
+    assert L.gpt2_tune_gemm_ln(0, dC.ptr, dX.ptr, dg.ptr, dbl.ptr, dW.ptr, sp, db.ptr, 1, N, K, 0) == 0

@@ -117,12 +117,14 @@ def test_prefill_forward_backends_agree(pkg, L, synth, model):
         assert rel_err(outs[be], outs["flash"]) <= 5e-3, be
 
 
-@pytest.mark.parametrize("backend,T", [("flash", 200), ("int8", 200), ("tiled", 33), ("int8", 512)])
-def test_fused_prefill_bit_identical(pkg, L, synth, model, backend, T):
+@pytest.mark.parametrize("backend,T,ln", [("flash", 200, -1), ("int8", 200, -1), ("tiled", 33, -1), ("int8", 512, -1),
+                                          ("flash", 200, 1), ("int8", 512, 2)])
+def test_fused_prefill_bit_identical(pkg, L, synth, model, backend, T, ln):
     """The fused launch sequence of the prefill (gelu and the residual adds in GEMM epilogues, the K/V
     cache fill inside the attention launch; the persistent trunk kernel switched off) equals the
     unfused reference sequence bit for bit: every layer's residual stream, the final LayerNorm, all
-    logits rows and the whole K/V cache."""
+    logits rows and the whole K/V cache.  ln >= 0 also runs LN1 -> QKV and LN2 -> fc as
+    LayerNorm-panel GEMMs with that config (at T where the plain GEMMs have one k group)."""
     ids = synth.token_ids(T, seed=T + 7)
     d_ids = pkg.Dev.from_numpy(np.asarray(ids, np.int32))
     if backend == "int8":
@@ -132,6 +134,7 @@ def test_fused_prefill_bit_identical(pkg, L, synth, model, backend, T):
     try:
         for fused in (1, 0):
             L.gpt2_tune_prefill_fused(fused)
+            L.gpt2_tune_gemm_ln_force(ln if fused else -1)
             scr, kv = pkg.Scratch(T), pkg.KVCache(T)
             logits, blocks, fin = pkg.Dev(T * V * 2), pkg.Dev(12 * T * E * 2), pkg.Dev(T * E * 2)
             caps = pkg.GPT2CapsGPU()
@@ -150,6 +153,7 @@ def test_fused_prefill_bit_identical(pkg, L, synth, model, backend, T):
             kv.free()
     finally:
         L.gpt2_tune_prefill_fused(1)
+        L.gpt2_tune_gemm_ln_force(-1)
         L.gpt2_tune_prefill_persistent(-1)
         if backend == "int8":
             L.gpt2_quant_free(C.byref(model.q))
