@@ -261,6 +261,14 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(uint16_t *__restrict__ C, con
 //   * one barrier per k-tile: the buffer refilled at step kt was last read at step kt-1.
 
 
+// Split-K across work-groups (k_gemm_sk), one copy per GPU: an arrival counter per output tile
+// (zero between launches: the last split of a tile resets it) and the splits' fp32 partial tiles.
+// Launches that use them must not overlap on one GPU; the library enqueues every kernel on one stream.
+constexpr int SK_TILES = 2048;
+constexpr size_t SK_WS_WORDS = (size_t)1 << 20;   // 64-bit words: 8 MiB (larger calls take another config)
+__device__ uint32_t g_sk_cnt[SK_TILES];
+__device__ uint64_t g_sk_ws[SK_WS_WORDS];
+
 // KS > 1 splits the k-tiles inside the work-group: KS groups of WN x WM waves, each with its own LDS
 // ring, run the same pipeline over consecutive 1/KS shares of K (so their barriers line up), and
 // groups 1.. add their accumulators into group 0's through LDS before the epilogue.
@@ -269,7 +277,8 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(uint16_t *__restrict__ C, con
 // EPI: the elementwise op fused into the epilogue (EPI_GELU; EPI_RESID adds resid, which may be C).
 // LNP (k_gemm_dl_ln): A is the LayerNorm of X[m0 .. m0+BM) (K = 768, gamma ln_g, beta ln_b), built
 // once per work-group into an LDS panel that holds all of the tile's A; the ring then carries W only.
-template <int BN, int BM, int WN, int WM, int S, bool QW, int KS, int U, int EPI, bool LNP>
+// SK > 1 (k_gemm_sk) splits K across SK work-groups per tile (see the split-K state below).
+template <int BN, int BM, int WN, int WM, int S, bool QW, int KS, int U, int EPI, bool LNP, int SK = 1>
 __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
                                         const void *__restrict__ Wv, const float *__restrict__ Ws,
                                         const uint16_t *__restrict__ bias, int M, int N, int K, int tiles_m,
@@ -287,6 +296,7 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
     constexpr int A_INS = RA / 1024, W_INS = W_BYTES / 1024;
     static_assert(A_BYTES % 1024 == 0 && W_BYTES % 1024 == 0, "1 KB load granules");
     static_assert(!LNP || (KS == 1 && EPI != EPI_RESID), "the LN panel form has one k group, no residual");
+    static_assert(SK == 1 || (KS == 1 && !LNP), "split-K across work-groups: one k group, no LN panel");
     constexpr int TOT = A_INS + W_INS, LO = TOT / NW, REM = TOT % NW, LMAX = LO + (REM ? 1 : 0);
     constexpr int WTN = BN / WN, WTM = BM / WM, TN = WTN / 16, TM = WTM / 16;
     static_assert(TN * 16 == WTN && TM * 16 == WTM, "wave tile is whole 16x16 blocks");
@@ -300,9 +310,12 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
     const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kg = wave_all / NW, wave = wave_all % NW;   // k group; wave inside the group
     char *smem = smem_all + kg * S * STAGE;
-    const int nk = K / BK / KS;                           // k-tiles per group
+    const int nk = K / BK / KS / SK;                      // k-tiles per group
     const size_t welt = QW ? 1 : 2;
-    const int tile = xcd_tile(blockIdx.x, ntiles);
+    // SK > 1: work-group b is split (vt % SK) of tile (vt / SK); the splits of a tile are consecutive
+    // in the XCD-aware order, so they run on one XCD
+    const int vt = xcd_tile(blockIdx.x, ntiles * SK);
+    const int tile = vt / SK, split = vt - tile * SK;
     const int n0 = (tile / tiles_m) * BN, m0 = (tile % tiles_m) * BM;
     const int wn0 = (wave / WM) * WTN, wm0 = (wave % WM) * WTM;
 
@@ -330,7 +343,7 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
         }
     }
 #pragma unroll
-    for (int j = 0; j < LMAX; ++j) gsrc[j] += (size_t)kg * nk * kstep[j];   // this group's share of K
+    for (int j = 0; j < LMAX; ++j) gsrc[j] += (size_t)(split * KS + kg) * nk * kstep[j];   // this group's share of K
     const int nld = (REM == 0 || wave < REM) ? LMAX : LO;   // wave-uniform
     auto issue = [&](int kt) {
         char *st = smem + (kt % S) * STAGE;
@@ -516,6 +529,62 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
                             acc[a][b][i] += red[(((g - 1) * NW + wave) * NACC + (a * TM + b) * 4 + i) * 64 + lane];
         }
     }
+    if constexpr (SK > 1) {
+        // Each split stores its fp32 accumulators into its slot of the workspace with device-scope
+        // stores (they reach memory shared by every XCD), waits for them, and bumps the tile's
+        // counter.  The split that arrives last sums all SK partial tiles in split order 0, 1, ..
+        // (the same order whichever split is last, so the result is deterministic), resets the
+        // counter for the next launch and runs the epilogue; the others are done.  Nothing waits on
+        // another work-group.
+        constexpr int NP = TN * TM * 2;                 // 64-bit accumulator pairs per lane
+        constexpr size_t SLOT = (size_t)NW * NP * 64;   // 64-bit words per split's partial tile
+        // the arrival count is broadcast through the ring, idle after the first barrier below (a
+        // second LDS object would cost the k-loop its alias information, see tests/test_asm_lds_dma.py)
+        uint32_t *s_arrived = reinterpret_cast<uint32_t *>(smem_all);
+        uint64_t *ws = g_sk_ws + (size_t)tile * SK * SLOT + (size_t)wave * NP * 64 + lane;
+        auto pack = [](float x, float y) { return (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32); };
+#pragma unroll
+        for (int a = 0; a < TN; ++a)
+#pragma unroll
+            for (int b = 0; b < TM; ++b)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    __hip_atomic_store(ws + split * SLOT + ((a * TM + b) * 2 + h) * 64,
+                                       pack(acc[a][b][2 * h], acc[a][b][2 * h + 1]), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        wait_vm<0>();
+        __syncthreads();
+        if (wave_all == 0)   // all 64 lanes add 1: one atomic of 64 (counts in units of 64)
+            *s_arrived = __builtin_amdgcn_readfirstlane(
+                __hip_atomic_fetch_add(g_sk_cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        __syncthreads();
+        if (__builtin_amdgcn_readfirstlane(*s_arrived) / 64 != SK - 1) return;
+        if (wave_all == 0) __hip_atomic_store(g_sk_cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint64_t part[SK][NP];
+#pragma unroll
+        for (int sp = 0; sp < SK; ++sp)
+#pragma unroll
+            for (int j = 0; j < NP; ++j)
+                part[sp][j] = sp == split ? 0 : __hip_atomic_load(ws + sp * SLOT + j * 64, __ATOMIC_RELAXED,
+                                                                  __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int a = 0; a < TN; ++a)
+#pragma unroll
+            for (int b = 0; b < TM; ++b) {
+                f32x4 sum;
+#pragma unroll
+                for (int sp = 0; sp < SK; ++sp) {
+                    f32x4 p = acc[a][b];
+                    if (sp != split) {
+                        const uint64_t lo = part[sp][(a * TM + b) * 2], hi = part[sp][(a * TM + b) * 2 + 1];
+                        p = f32x4{__uint_as_float((uint32_t)lo), __uint_as_float((uint32_t)(lo >> 32)),
+                                  __uint_as_float((uint32_t)hi), __uint_as_float((uint32_t)(hi >> 32))};
+                    }
+                    sum = sp == 0 ? p : sum + p;
+                }
+                acc[a][b] = sum;
+            }
+    }
     // Epilogue: lane holds D[n][m] for n = nb..nb+3, m = mrow.
     if (!vec_store) {
         // Rows of C that are not 8-byte aligned (odd N: the tied head's 50257 columns): the tile
@@ -595,6 +664,17 @@ __global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restri
                                                       nullptr, nullptr);
 }
 
+// k_gemm_dl with K split over SK work-groups per tile (grid = tiles x SK): for tiles large enough
+// to read few bytes per FLOP, which alone would leave CUs idle.
+template <int BN, int BM, int WN, int WM, int S, bool QW, int U, int EPI, int SK>
+__global__ __launch_bounds__(WN *WM * 64) void k_gemm_sk(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
+                                                    const void *__restrict__ Wv, const float *__restrict__ Ws,
+                                                    const uint16_t *__restrict__ bias, int M, int N, int K,
+                                                    int tiles_m, int ntiles, int vec_store, const uint16_t *resid) {
+    gemm_dl<BN, BM, WN, WM, S, QW, 1, U, EPI, false, SK>(C, A, Wv, Ws, bias, M, N, K, tiles_m, ntiles, vec_store,
+                                                         resid, nullptr, nullptr);
+}
+
 // C = LayerNorm(X; ln_g, ln_b) . W^T (+ bias) (then gelu for EPI_GELU), K = 768: the prefill's
 // LN1 -> QKV and LN2 -> fc without the LayerNorm launch and its round trip through memory.  Each
 // work-group normalizes its BM rows of X itself (the rows are recomputed by every work-group of the
@@ -664,6 +744,7 @@ struct GemmCfg {
     GemmFn fused[2][2];  // [int8][gelu, residual]: fused-epilogue kernels, on the configs the prefill picks
     bool dl;             // direct-to-LDS pipeline
     const char *name;
+    int sk;              // > 1: K split over sk work-groups per tile (k_gemm_sk; grid = tiles x sk)
 };
 
 #define G2_NOFUSE {{nullptr, nullptr}, {nullptr, nullptr}}
@@ -690,6 +771,13 @@ struct GemmCfg {
      "dl_bn" #BN "_bm" #BM "_w" #WN "x" #WM "_s" #S "_k" #KS "_u" #U}
 #define G2_DCFGU(BN, BM, WN, WM, S, KS, U) G2_DCFGU_(BN, BM, WN, WM, S, KS, U, G2_NOFUSE)
 #define G2_DCFGUF(BN, BM, WN, WM, S, KS, U) G2_DCFGU_(BN, BM, WN, WM, S, KS, U, G2_FUSE(BN, BM, WN, WM, S, KS, U))
+// ... and K split over SK work-groups per tile: K % (64 U SK) == 0, at least S-U k-tiles per split.
+#define G2_SKCFG(BN, BM, WN, WM, S, U, SK)                                                                          \
+    {BN, BM, 64 * U * SK, 64 * SK * (S - U), 64 * WN * WM, k_gemm_sk<BN, BM, WN, WM, S, false, U, EPI_NONE, SK>,     \
+     k_gemm_sk<BN, BM, WN, WM, S, true, U, EPI_NONE, SK>,                                                          \
+     {{k_gemm_sk<BN, BM, WN, WM, S, false, U, EPI_GELU, SK>, k_gemm_sk<BN, BM, WN, WM, S, false, U, EPI_RESID, SK>}, \
+      {k_gemm_sk<BN, BM, WN, WM, S, true, U, EPI_GELU, SK>, k_gemm_sk<BN, BM, WN, WM, S, true, U, EPI_RESID, SK>}},  \
+     true, "sk_bn" #BN "_bm" #BM "_w" #WN "x" #WM "_s" #S "_u" #U "_x" #SK, SK}
 static const GemmCfg kCfgs[] = {
     G2_DCFGF(96, 64, 2, 4, 4),      // 0: 8 waves, wave tile 48x16
     G2_DCFG(128, 64, 4, 2, 3),      // 1: 8 waves, wave tile 32x32 (vocabulary-sized N)
@@ -740,9 +828,17 @@ static const GemmCfg kCfgs[] = {
     G2_DCFGUF(48, 32, 3, 1, 4, 4, 2),   // 45: four k groups of 3 waves, 16x32 wave tiles (INT8 mlp-proj)
     G2_DCFG(128, 64, 4, 2, 2),          // 46: as 1, double-buffered (49 KB of LDS: three work-groups per CU)
     G2_DCFGUF(32, 32, 1, 2, 4, 4, 1),   // 47: as 14 (four k groups of 2 waves), with the fused epilogues
+    // split K over work-groups (k_gemm_sk): large tiles (half the L2 bytes per FLOP of the 48x32 tiles)
+    // and still 256+ work-groups.  Measured 30-50% slower than the picks above at P=512: the partial
+    // tiles cross XCDs through memory (the stores' drain, then the last split's loads: ~3 us of a
+    // 5-10 us launch), so no pick uses them.
+    G2_SKCFG(96, 64, 3, 2, 4, 2, 2),    // 48: 6 waves, wave tile 32x32, 2 splits
+    G2_SKCFG(96, 64, 6, 2, 4, 2, 2),    // 49: 12 waves, wave tile 16x32, 2 splits
+    G2_SKCFG(96, 64, 6, 2, 4, 2, 4),    // 50: as 49, 4 splits
+    G2_SKCFG(64, 64, 2, 2, 4, 2, 2),    // 51: 4 waves, wave tile 32x32, 2 splits
 };
 static const int kNumCfgs = (int)(sizeof(kCfgs) / sizeof(kCfgs[0]));
-static_assert(sizeof(kCfgs) / sizeof(kCfgs[0]) == 48, "the pick table names configs by index");
+static_assert(sizeof(kCfgs) / sizeof(kCfgs[0]) == 52, "the pick table names configs by index");
 
 // Any K % 8 == 0 (int8: K % 16 == 0): predicated loads, one k-tile of prefetch.
 #define G2_GCFG(BN, BM, WN, WM) \
@@ -777,6 +873,14 @@ static int g_force_cfg = -2;  // -2: not read yet; -1: table
 
 static bool cfg_fits(int c, int K) { return K % kCfgs[c].kmul == 0 && K >= kCfgs[c].kmin; }
 
+// A split-K config also needs its tiles within the counters and its partial tiles within the workspace.
+static bool sk_room(const GemmCfg &g, int M, int N) {
+    if (g.sk <= 1) return true;
+    const long tiles = (long)cdiv(M, g.bm) * cdiv(N, g.bn);
+    return tiles <= SK_TILES && tiles * g.sk * g.bn * g.bm / 2 <= (long)SK_WS_WORDS;
+}
+static bool cfg_usable(int c, int M, int N, int K) { return cfg_fits(c, K) && sk_room(kCfgs[c], M, N); }
+
 // The config forced by gpt2_tune_gemm_force or the GPT2_GEMM_CFG environment variable, or -1.
 static int forced_cfg() {
     if (g_force_cfg == -2) {
@@ -809,7 +913,7 @@ static const int kPick[5][4][2] = {
 };
 
 static int pick_cfg(int M, int N, int K, bool qw = false) {
-    if (forced_cfg() >= 0 && cfg_fits(g_force_cfg, K)) return g_force_cfg;
+    if (forced_cfg() >= 0 && cfg_usable(g_force_cfg, M, N, K)) return g_force_cfg;
     int shape = -1;
     if (N == 2304 && K == 768) shape = 0;            // QKV
     else if (N == 768 && K == 768) shape = 1;        // attn-proj
@@ -818,7 +922,7 @@ static int pick_cfg(int M, int N, int K, bool qw = false) {
     if (shape >= 0 && M >= 2 && M <= 1024) {
         const int bucket = M <= 64 ? 0 : M <= 128 ? 1 : M <= 256 ? 2 : M <= 512 ? 3 : 4;
         const int c = kPick[bucket][shape][qw ? 1 : 0];
-        if (cfg_fits(c, K)) return c;
+        if (cfg_usable(c, M, N, K)) return c;
     }
     // Other shapes: vocabulary-sized N (the tied head, 50257 rows of W) has many tiles per CU, where
     // large tiles win on L2 bytes per FLOP (M=512: 128x64 83 us, 256x128 88, 128x128 94, 48-row
@@ -850,8 +954,8 @@ static void launch_gemm(const GemmCfg &g, GemmFn fn, uint16_t *C, const uint16_t
     const int tiles_m = cdiv(M, g.bm), tiles_n = cdiv(N, g.bn);
     const int ntiles = tiles_m * tiles_n;
     const int vec = (N % 4 == 0) && (((uintptr_t)C & 7u) == 0);
-    hipLaunchKernelGGL(fn, dim3(ntiles), dim3(g.threads), 0, stream(), C, A, W, Ws, bias, M, N, K, tiles_m, ntiles, vec,
-                       resid);
+    hipLaunchKernelGGL(fn, dim3(ntiles * (g.sk > 1 ? g.sk : 1)), dim3(g.threads), 0, stream(), C, A, W, Ws, bias, M, N,
+                       K, tiles_m, ntiles, vec, resid);
 }
 
 static bool gemm_args(const char *who, const void *C, const void *A, const void *W, int M, int N, int K) {
@@ -871,7 +975,7 @@ void gemm(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const 
     }
     // K == 0 (an empty sum, C = bias or 0) falls through to the generic kernel.
     if (K > 0 && mfma_ok(A, W, K, qw)) {
-        const int c = (cfg >= 0 && cfg < kNumCfgs && cfg_fits(cfg, K)) ? cfg : pick_cfg(M, N, K, qw);
+        const int c = (cfg >= 0 && cfg < kNumCfgs && cfg_usable(cfg, M, N, K)) ? cfg : pick_cfg(M, N, K, qw);
         const GemmCfg &g = c >= 0 ? kCfgs[c] : kGuardCfgs[(long)cdiv(N, 64) * cdiv(M, 64) >= 256 ? 0 : 1];
         launch_gemm(g, qw ? g.int8 : g.fp16, C, A, W, Ws, bias, M, N, K);
         check_launch(qw ? "k_gemm_mfma<int8>" : "k_gemm_mfma<fp16>");

@@ -8,9 +8,14 @@
 
 extern "C" {
 
+// Tuning hook of libgpt2amd.so (csrc/gemm.hip): one GEMM on a fixed tile config.
+void gpt2_tune_gemm_run(int cfg, gpt2_half *C, const gpt2_half *A, const void *W, const float *Ws,
+                        const gpt2_half *bias, int M, int N, int K);
+
 // One timed operation: kind 0 = fp16 GEMM (gpt2_matmul_tiled), 1 = INT8 GEMM (gpt2_matmul_int8),
 // 2 = fp16 GEMV (gpt2_gemv_fp16), 3 = INT8 GEMV (gpt2_gemv_int8), 4 = causal prefill attention
-// (gpt2_attention_flash: C = att, A = qkv, M = T).
+// (gpt2_attention_flash: C = att, A = qkv, M = T), 16 + c = the GEMM on tile config c
+// (gpt2_tune_gemm_run; INT8 weights when Ws is not NULL), for sweeps that mix configs in one step.
 typedef struct {
     int kind;
     gpt2_half *C;
@@ -27,7 +32,8 @@ static void run_op(const GPT2BenchOp &o) {
         case 1: gpt2_matmul_int8(o.C, o.A, (const int8_t *)o.W, o.Ws, o.bias, o.M, o.N, o.K); break;
         case 2: gpt2_gemv_fp16(o.C, o.A, (const gpt2_half *)o.W, o.bias, o.N, o.K); break;
         case 4: gpt2_attention_flash(o.C, o.A, o.M, GPT2_N_EMBD, GPT2_N_HEAD, GPT2_HEAD_DIM); break;
-        default: gpt2_gemv_int8(o.C, o.A, (const int8_t *)o.W, o.Ws, o.bias, o.N, o.K); break;
+        case 3: gpt2_gemv_int8(o.C, o.A, (const int8_t *)o.W, o.Ws, o.bias, o.N, o.K); break;
+        default: gpt2_tune_gemm_run(o.kind - 16, o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K); break;
     }
 }
 

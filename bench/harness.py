@@ -19,7 +19,8 @@ _i, _sz = C.c_int, C.c_size_t
 
 class GPT2BenchOp(C.Structure):
     """One timed operation (bench.hip): kind 0 fp16 GEMM, 1 INT8 GEMM, 2 fp16 GEMV, 3 INT8 GEMV,
-    4 causal prefill attention (C = att, A = qkv, M = T)."""
+    4 causal prefill attention (C = att, A = qkv, M = T), 16 + c the GEMM on tile config c (INT8
+    when Ws is set)."""
     _fields_ = [("kind", C.c_int), ("C", _vp), ("A", _vp), ("W", _vp), ("Ws", _vp), ("bias", _vp),
                 ("M", C.c_int), ("N", C.c_int), ("K", C.c_int)]
 

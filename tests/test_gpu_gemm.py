@@ -372,3 +372,31 @@ def test_ln_panel_gemm(pkg, L, kind, M, N):
     # shapes the LayerNorm panel does not take: the caller falls back to the two launches
     assert L.gpt2_tune_gemm_ln(0, dC.ptr, dX.ptr, dg.ptr, dbl.ptr, dW.ptr, sp, db.ptr, M, N // 2, K // 2, 0) == 0
     assert L.gpt2_tune_gemm_ln(0, dC.ptr, dX.ptr, dg.ptr, dbl.ptr, dW.ptr, sp, db.ptr, 1, N, K, 0) == 0
+
+
+def test_split_k_repeatable(pkg, L):
+    """The split-K configs (K split over several work-groups per tile, the fp32 partials summed in
+    split order by the last work-group to arrive, which also resets the tile's counter): a call
+    repeated after a call with another tile count gives the same bits, and agrees with the oracle;
+    fp16 and INT8."""
+    rng = np.random.default_rng(21)
+    sk = [c for c in range(L.gpt2_tune_gemm_count()) if L.gpt2_tune_gemm_name(c).decode().startswith("sk_")]
+    assert sk
+    big = (512, 768, 3072)
+    small = (65, 200, 3072)
+    data = {}
+    for M, N, K in (big, small):
+        A, W, b = f16v(rng, (M, K), 1.0), f16v(rng, (N, K), 0.05), f16v(rng, N, 0.01)
+        q, s, _ = oracle.quantize_fp16_view(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.05))
+        data[(M, N, K)] = (A, W, b, q, s)
+    for cfg in sk:
+        name = L.gpt2_tune_gemm_name(cfg).decode()
+        for kind in ("fp16", "int8"):
+            runs = []
+            for shape in (big, small, big):
+                A, W, b, q, s = data[shape]
+                runs.append(gemm(pkg, L, A, W if kind == "fp16" else None, b, cfg=cfg, kind=kind, q=q, s=s))
+            assert np.array_equal(runs[0], runs[2]), f"{name} {kind}: repeated call differs"
+            A, W, b, q, s = data[big]
+            ref = oracle.matmul(A, W if kind == "fp16" else oracle.dequantize(q, s), b)
+            tol_check(runs[0], ref)
