@@ -780,7 +780,7 @@ struct GemmCfg {
      true, "sk_bn" #BN "_bm" #BM "_w" #WN "x" #WM "_s" #S "_u" #U "_x" #SK, SK}
 static const GemmCfg kCfgs[] = {
     G2_DCFGF(96, 64, 2, 4, 4),      // 0: 8 waves, wave tile 48x16
-    G2_DCFG(128, 64, 4, 2, 3),      // 1: 8 waves, wave tile 32x32 (vocabulary-sized N)
+    G2_DCFGF(128, 64, 4, 2, 3),     // 1: 8 waves, wave tile 32x32 (vocabulary-sized N; INT8 fc at M=1024)
     G2_DCFGF(32, 64, 1, 4, 4),      // 2: 4 waves, wave tile 32x16
     G2_DCFGF(64, 32, 2, 2, 4),      // 3: 4 waves, wave tile 32x16
     G2_DCFG(96, 64, 2, 2, 6),       // 4: 4 waves, wave tile 48x32
@@ -903,13 +903,14 @@ static int forced_cfg() {
 //     shape up to M=256 (M=64 QKV: 3.95 against 6.3 us), where each wave widens fewer W rows;
 //   * M in (256, 512] (the P=512 headline): 48-row W tiles, chosen inside the step;
 //   * M up to 1024: 96x64 / 128x128 tiles for fp16 QKV and fc (10.4 / 10.9 us), 64x64 for mlp-proj
-//     (12.9 against 16.5 us), 48x64 with two k groups (36) for attn-proj and the INT8 GEMMs.
+//     (12.9 against 16.5 us), 48x64 with two k groups (36) for attn-proj and the INT8 GEMMs, 128x64
+//     for INT8 fc (12.0 against 13.4 us for 48x32, isolated).
 static const int kPick[5][4][2] = {
     /* M <= 64   */ {{8, 47}, {8, 47}, {8, 47}, {47, 47}},
     /* M <= 128  */ {{8, 39}, {8, 47}, {8, 39}, {47, 47}},
     /* M <= 256  */ {{29, 36}, {8, 47}, {40, 36}, {47, 45}},
     /* M <= 512  */ {{35, 35}, {25, 31}, {26, 35}, {23, 45}},
-    /* M <= 1024 */ {{0, 35}, {36, 36}, {6, 35}, {5, 36}},
+    /* M <= 1024 */ {{0, 35}, {36, 36}, {6, 1}, {5, 36}},
 };
 
 static int pick_cfg(int M, int N, int K, bool qw = false) {
