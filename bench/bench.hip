@@ -11,11 +11,16 @@ extern "C" {
 // Tuning hook of libgpt2amd.so (csrc/gemm.hip): one GEMM on a fixed tile config.
 void gpt2_tune_gemm_run(int cfg, gpt2_half *C, const gpt2_half *A, const void *W, const float *Ws,
                         const gpt2_half *bias, int M, int N, int K);
+int gpt2_tune_gemm_fused(gpt2_half *C, const gpt2_half *A, const void *W, const float *Ws, const gpt2_half *bias,
+                         int M, int N, int K, int epi, const gpt2_half *resid);
 
 // One timed operation: kind 0 = fp16 GEMM (gpt2_matmul_tiled), 1 = INT8 GEMM (gpt2_matmul_int8),
 // 2 = fp16 GEMV (gpt2_gemv_fp16), 3 = INT8 GEMV (gpt2_gemv_int8), 4 = causal prefill attention
-// (gpt2_attention_flash: C = att, A = qkv, M = T), 16 + c = the GEMM on tile config c
-// (gpt2_tune_gemm_run; INT8 weights when Ws is not NULL), for sweeps that mix configs in one step.
+// (gpt2_attention_flash: C = att, A = qkv, M = T), 5 = LayerNorm (gpt2_layernorm: C = out, A = x,
+// W = gamma, bias = beta, M rows of K), 6 = the GEMM with the residual add fused (C = C + A.W^T + b,
+// gpt2_tune_gemm_fused epi 2), 7 = residual add (gpt2_add: C += A, M*N elements), 16 + c = the GEMM
+// on tile config c (gpt2_tune_gemm_run; INT8 weights when Ws is not NULL), for sweeps that mix
+// configs in one step.
 typedef struct {
     int kind;
     gpt2_half *C;
@@ -33,6 +38,9 @@ static void run_op(const GPT2BenchOp &o) {
         case 2: gpt2_gemv_fp16(o.C, o.A, (const gpt2_half *)o.W, o.bias, o.N, o.K); break;
         case 4: gpt2_attention_flash(o.C, o.A, o.M, GPT2_N_EMBD, GPT2_N_HEAD, GPT2_HEAD_DIM); break;
         case 3: gpt2_gemv_int8(o.C, o.A, (const int8_t *)o.W, o.Ws, o.bias, o.N, o.K); break;
+        case 5: gpt2_layernorm(o.C, o.A, (const gpt2_half *)o.W, o.bias, o.M, o.K); break;
+        case 6: gpt2_tune_gemm_fused(o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K, g2::EPI_RESID, o.C); break;
+        case 7: gpt2_add(o.C, o.A, (size_t)o.M * o.N); break;
         default: gpt2_tune_gemm_run(o.kind - 16, o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K); break;
     }
 }
