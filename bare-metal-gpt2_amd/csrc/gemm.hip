@@ -554,12 +554,12 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
                                        __HIP_MEMORY_SCOPE_AGENT);
         wait_vm<0>();
         __syncthreads();
-        if (wave_all == 0)   // all 64 lanes add 1: one atomic of 64 (counts in units of 64)
-            *s_arrived = __builtin_amdgcn_readfirstlane(
-                __hip_atomic_fetch_add(g_sk_cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        // One thread adds 1, so the count is exact whatever the compiler does with atomics of many
+        // lanes (a straight-line branch: no loop runs through this barrier).
+        if (tid == 0) *s_arrived = __hip_atomic_fetch_add(g_sk_cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
-        if (__builtin_amdgcn_readfirstlane(*s_arrived) / 64 != SK - 1) return;
-        if (wave_all == 0) __hip_atomic_store(g_sk_cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_readfirstlane(*s_arrived) != SK - 1) return;
+        if (tid == 0) __hip_atomic_store(g_sk_cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         uint64_t part[SK][NP];
 #pragma unroll
         for (int sp = 0; sp < SK; ++sp)

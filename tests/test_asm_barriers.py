@@ -12,7 +12,7 @@ import re
 
 import pytest
 
-from asm_util import device_asm
+from asm_util import device_asm, functions
 
 
 def blocks(lines):
@@ -90,3 +90,19 @@ def test_persistent_kernels_have_uniform_loops_around_barriers(src):
     asm = device_asm(src)
     assert "s_barrier" in asm and "Loop Header" in asm
     assert hazardous_loops(asm) == []
+
+
+def test_persistent_prefill_counts_one_atomic_per_wave():
+    """The persistent prefill's ticket fetch and counter bumps are made by all 64 lanes of wave 0 with
+    the value 1 and read as multiples of 64 (a ticket is old / 64), so they are exact only if each
+    wave's adds reach memory as ONE atomic of 64: interleaved single-lane adds of two work-groups
+    could hand both the same ticket.  The compiler emits that single atomic (the active-lane count
+    from s_bcnt1 added by one lane); this checks every atomic add of the kernel is in that form."""
+    fns = {k: v for k, v in functions(device_asm("prefill.hip")).items() if "k_prefill_persist" in k}
+    assert fns
+    for name, lines in fns.items():
+        sites = [i for i, x in enumerate(lines) if x.strip().startswith("global_atomic_add")]
+        assert sites, name
+        for i in sites:
+            window = [x.strip() for x in lines[max(0, i - 5):i]]
+            assert any(x.startswith("s_bcnt1_i32_b64") for x in window), f"{name}: per-lane atomic add at line {i}"
