@@ -18,8 +18,10 @@
 //     are mapped to keys {4g..4g+3} of the chunk's first tile and {16+4g..16+4g+3} of its second --
 //     exactly the keys the lane already holds P for -- so P is the B operand as it comes out of the
 //     softmax, converted to fp16 in registers.  V^T (keys contiguous per dim) is the A operand: each
-//     wave transposes its chunk's 32 x 64 V block through its own LDS tile (a lane packs four keys
-//     of one dim into one 8-byte write; a fragment is two 8-byte reads).
+//     wave stores its chunk's 32 x 64 V block row-major in its own LDS tile (16-byte writes, rows
+//     padded to 160 B so that neither the writes nor the reads below meet a bank conflict) and
+//     reads each fragment half with gfx950's transposing LDS read, ds_read_b64_tr_b16: within 16
+//     lanes, lane 4k+a names 4 dims of key k and lane 4a+b receives dim b of those 4 keys.
 //   * Softmax in the log2 domain (p = 2^(s*log2(e)/8 - m) as one FMA and v_exp_f32), the row maximum
 //     shared by the lane groups of a query each chunk through the VALU lane swaps (no LDS
 //     permutes); the causal mask is applied only to chunks that cross the diagonal.  The
@@ -36,7 +38,7 @@ namespace g2 {
 constexpr int AP_QB = 16;                      // queries per work-group
 constexpr int AP_CK = 32;                      // keys per chunk
 constexpr int AP_W = 4;                        // waves per work-group
-constexpr int AP_RS = 2 * AP_CK + 8;           // bytes per V^T row in LDS (32 keys + 8 B pad)
+constexpr int AP_RV = 160;                     // bytes per V row in LDS (64 dims + 32 B pad)
 
 // 2^x on the hardware exp unit (no denormal-range fix-up: arguments here are <= 0 and a result
 // below 2^-126 may flush to zero, which is below anything an fp16 probability can hold).
@@ -57,9 +59,23 @@ __device__ __forceinline__ float group_sum(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// gfx950's transposing LDS read of 8 bytes (ds_read_b64_tr_b16): within each 16 lanes, lane 4k+a
+// supplies the address of 4 consecutive halves, and lane 4a+b receives half b of the addresses of
+// lanes a, 4+a, 8+a, 12+a, in that order (layout checked on the GPU).
+__device__ __forceinline__ f16x4 tr_read(const char *p) {
+#if defined(__HIP_DEVICE_COMPILE__)   // LDS address-space pointers exist only in the device pass
+    typedef short i16x4 __attribute__((ext_vector_type(4)));
+    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4 *)(p));
+    return __builtin_bit_cast(f16x4, v);
+#else
+    (void)p;
+    return f16x4{};
+#endif
+}
+
 // LDS of one attention block (four waves).
 struct AttnLds {
-    char vt_all[AP_W][GPT2_HEAD_DIM * AP_RS];
+    char vt_all[AP_W][AP_CK * AP_RV];
     float mrg_m[AP_W][AP_QB], mrg_l[AP_W][AP_QB];
     f32x4 mrg_o[AP_W][AP_W][64];    // [source wave][dim group][lane]
 };
@@ -158,37 +174,20 @@ __device__ __forceinline__ void attn_block(AttnLds &lds, uint16_t *__restrict__ 
 #pragma unroll
         for (int e = 0; e < 8; e += 2) ps = __builtin_amdgcn_fdot2(f16x2{pb[e], pb[e + 1]}, f16x2{1, 1}, ps, false);
         lsum = fmaf(lsum, corr, ps);
-        // ---- V^T of the chunk into this wave's LDS tile: row d holds keys 0..31
-        {
-            uint32_t u[4][4];   // u[i][j]: dims vd+2j (low half), vd+2j+1 (high half) of key vk+i
+        // ---- the chunk's V rows into this wave's LDS tile, row-major: key vk + i, dims vd .. vd+7
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint4 b = __builtin_bit_cast(uint4, R.v[i]);
-                u[i][0] = b.x;
-                u[i][1] = b.y;
-                u[i][2] = b.z;
-                u[i][3] = b.w;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                // dim vd+2j: low halves of the four keys; dim vd+2j+1: high halves
-                const uint2 lo = {__builtin_amdgcn_perm(u[1][j], u[0][j], 0x05040100u),
-                                  __builtin_amdgcn_perm(u[3][j], u[2][j], 0x05040100u)};
-                const uint2 hi = {__builtin_amdgcn_perm(u[1][j], u[0][j], 0x07060302u),
-                                  __builtin_amdgcn_perm(u[3][j], u[2][j], 0x07060302u)};
-                *reinterpret_cast<uint2 *>(vt + (vd + 2 * j) * AP_RS + 2 * vk) = lo;
-                *reinterpret_cast<uint2 *>(vt + (vd + 2 * j + 1) * AP_RS + 2 * vk) = hi;
-            }
-        }
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<f16x8 *>(vt + (vk + i) * AP_RV + 2 * vd) = R.v[i];
         // The tile is written and read by this wave only: waiting for its own LDS writes is enough
         // (the "memory" clobber keeps the compiler from moving the reads above the writes).
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
         for (int dg = 0; dg < 4; ++dg) {
-            const char *row = vt + (16 * dg + jq) * AP_RS;
-            const uint2 lo = *reinterpret_cast<const uint2 *>(row + 8 * g);        // keys 4g .. 4g+3
-            const uint2 hi = *reinterpret_cast<const uint2 *>(row + 32 + 8 * g);   // keys 16+4g .. 16+4g+3
-            const f16x8 va = __builtin_bit_cast(f16x8, uint4{lo.x, lo.y, hi.x, hi.y});
+            // lane jq = 4q + r of group g names dims 16dg + 4r .. +3 of key (base + q); it receives
+            // dim 16dg + jq of keys base .. base+3 (base 4g: the lo half, 16 + 4g: the hi half)
+            const char *col = vt + 2 * (16 * dg + 4 * (jq & 3));
+            const f16x4 lo = tr_read(col + (4 * g + (jq >> 2)) * AP_RV);
+            const f16x4 hi = tr_read(col + (16 + 4 * g + (jq >> 2)) * AP_RV);
+            const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             o[dg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[dg] * corr, 0, 0, 0);
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // reads done before the next chunk's writes
