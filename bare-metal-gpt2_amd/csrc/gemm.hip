@@ -234,7 +234,7 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(uint16_t *__restrict__ C, con
                 o[i] = f2h(v + bs[i]);
             }
             uint16_t *dst = C + (size_t)m * N + nb;
-            if (vec_store && nb + 3 < N) {
+            if ((vec_store & 1) && nb + 3 < N) {
                 const uint2 pk = {(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
                 *reinterpret_cast<uint2 *>(dst) = pk;
             } else {
@@ -282,9 +282,12 @@ template <int BN, int BM, int WN, int WM, int S, bool QW, int KS, int U, int EPI
 __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t *__restrict__ A,
                                         const void *__restrict__ Wv, const float *__restrict__ Ws,
                                         const uint16_t *__restrict__ bias, int M, int N, int K, int tiles_m,
-                                        int ntiles, int vec_store, const uint16_t *resid,
+                                        int ntiles, int flags, const uint16_t *resid,
                                         const uint16_t *__restrict__ ln_g, const uint16_t *__restrict__ ln_b) {
 #if defined(__HIP_DEVICE_COMPILE__)   // LDS address-space pointers exist only in the device pass
+    // flags: bit 0 = C rows are 8-byte aligned (vector stores); bits 4-7 = gn, the XCD block grid
+    // (see below; 0 = contiguous runs of tiles per XCD).
+    const int vec_store = flags & 1, gn = (flags >> 4) & 15;
     constexpr int NW = WN * WM;
     constexpr int BK = 64;
     constexpr int A_BYTES = BM * BK * 2;        // fp16 A tile: rows of 128 B (8 chunks)
@@ -315,7 +318,17 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
     // SK > 1: work-group b is split (vt % SK) of tile (vt / SK); the splits of a tile are consecutive
     // in the XCD-aware order, so they run on one XCD
     const int vt = xcd_tile(blockIdx.x, ntiles * SK);
-    const int tile = vt / SK, split = vt - tile * SK;
+    int tile = vt / SK;
+    const int split = vt - tile * SK;
+    if (SK == 1 && gn) {
+        // 2-D XCD blocks: the tile grid (tiles_n x tiles_m) is cut into gn x (8 / gn) blocks and XCD x
+        // (work-group b runs on XCD b % 8) takes block (x % gn, x / gn), m fastest inside it, so its L2
+        // fetches W rows for tiles_n / gn n-tiles and A rows for 8 tiles_m / gn m-tiles instead of all
+        // of A (the host sets gn only where both divide and ntiles % 8 == 0).
+        const int xcd = blockIdx.x & 7, i = blockIdx.x >> 3;
+        const int bn_ = ntiles / tiles_m / gn, bm_ = tiles_m * gn / 8;
+        tile = ((xcd % gn) * bn_ + i / bm_) * tiles_m + (xcd / gn) * bm_ + i % bm_;
+    }
     const int n0 = (tile / tiles_m) * BN, m0 = (tile % tiles_m) * BM;
     const int wn0 = (wave / WM) * WTN, wm0 = (wave % WM) * WTM;
 
@@ -950,13 +963,34 @@ static bool mfma_ok(const void *A, const void *W, int K, bool qw) {
     return (K % 8) == 0 && aligned16(A) && aligned16(W);
 }
 
+// The XCD block grid gn for a direct-to-LDS launch (0: contiguous runs of tiles per XCD).  Each XCD's
+// L2 fetches the W rows of its n-tiles and the A rows of its m-tiles once; with contiguous runs every
+// XCD covers all m-tiles, so A (at K = 3072 the 3 MB activation of mlp-proj) is fetched by all eight.
+// gn x (8 / gn) blocks minimize those bytes.  Measured on MI355X at P=512: mlp-proj (K = 3072) moves
+// 26% fewer bytes past its L2s at the same speed; attn-proj (K = 768) ran 4.5% slower, so shorter K
+// keeps the contiguous runs.
+static int xcd_blocks(const GemmCfg &g, int tiles_m, int tiles_n, int K, bool qw) {
+    if (!g.dl || g.sk > 1 || K < 2048 || (tiles_m * tiles_n) % 8) return 0;
+    const long wrow = (long)g.bn * (qw ? 1 : 2), arow = (long)g.bm * 2;   // bytes per k of one n-tile / m-tile
+    int best = 0;
+    long best_cost = 0;
+    for (int gn = 8; gn >= 1; gn /= 2) {
+        const int gm = 8 / gn;
+        if (tiles_n % gn || tiles_m % gm) continue;
+        const long cost = tiles_n / gn * wrow + tiles_m / gm * arow;
+        if (!best || cost < best_cost) { best = gn; best_cost = cost; }
+    }
+    // gn = 8 is what contiguous runs already give when 8 divides tiles_n
+    return (best == 8 && tiles_n % 8 == 0) ? 0 : best;
+}
+
 static void launch_gemm(const GemmCfg &g, GemmFn fn, uint16_t *C, const uint16_t *A, const void *W, const float *Ws,
                         const uint16_t *bias, int M, int N, int K, const uint16_t *resid = nullptr) {
     const int tiles_m = cdiv(M, g.bm), tiles_n = cdiv(N, g.bn);
     const int ntiles = tiles_m * tiles_n;
     const int vec = (N % 4 == 0) && (((uintptr_t)C & 7u) == 0);
     hipLaunchKernelGGL(fn, dim3(ntiles * (g.sk > 1 ? g.sk : 1)), dim3(g.threads), 0, stream(), C, A, W, Ws, bias, M, N,
-                       K, tiles_m, ntiles, vec, resid);
+                       K, tiles_m, ntiles, vec | (xcd_blocks(g, tiles_m, tiles_n, K, Ws != nullptr) << 4), resid);
 }
 
 static bool gemm_args(const char *who, const void *C, const void *A, const void *W, int M, int N, int K) {

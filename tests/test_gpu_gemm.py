@@ -161,10 +161,12 @@ def test_generic_path_unaligned_a(pkg, L):
 
 
 def test_every_tile_config(pkg, L):
-    """Every tile config on shapes whose K it accepts (K % (64*depth) == 0), ragged M and N, plus
-    shapes no config accepts (the guarded kernel)."""
+    """Every tile config on shapes whose K it accepts (K % (64*depth) == 0), ragged M and N, odd N
+    (C rows not 8-byte aligned: the staged epilogue), plus shapes no config accepts (the guarded
+    kernel)."""
     rng = np.random.default_rng(11)
-    for M, N, K in [(100, 200, 136), (512, 768, 768), (7, 300, 768), (77, 130, 3072), (33, 96, 64)]:
+    for M, N, K in [(100, 200, 136), (512, 768, 768), (7, 300, 768), (77, 130, 3072), (33, 96, 64),
+                    (130, 1001, 768)]:
         A, W, b = f16v(rng, (M, K), 1.0), f16v(rng, (N, K), 0.05), f16v(rng, N, 0.01)
         ref = oracle.matmul(A, W, b)
         q, s, _ = oracle.quantize_fp16_view(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.05))
