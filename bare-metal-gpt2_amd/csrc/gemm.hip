@@ -429,11 +429,14 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
     // trip after it.  The loads are unconditional, one element per register, at clamped indices
     // (out-of-range columns and rows are dropped in the epilogue; without a bias, A[0] stands in and
     // is not used): a branch around a load, or converting or packing the value before the
-    // epilogue, would make the wave wait for the load right here.  (The residual may alias C: this
-    // lane is the only one that writes these elements, in the epilogue.)
+    // epilogue, would make the wave wait for the load right here.  The residual (fused only where C
+    // rows are 8-byte aligned) is one 8-byte load of the lane's 4 columns per output block, by the
+    // k group that stores (4 scattered 2-byte loads per block, in every k group, cost 0.8-2.3 us per
+    // launch in request traffic).  (The residual may alias C: this lane is the only one that writes
+    // these elements, in the epilogue.)
     uint32_t bs_e[TN][4];            // fp16 bias bits, zero-extended
     float sc_e[TN][4];
-    uint32_t rs_e[TN][TM][4];        // fp16 residual bits
+    uint2 rs2[TN][TM];               // fp16 residual bits, 4 columns packed
 #pragma unroll
     for (int a = 0; a < TN; ++a) {
         const int nb = n0 + wn0 + a * 16 + lgrp * 4;
@@ -445,14 +448,17 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
             bs_e[a][i] = *(bias ? bias + n : A);
         }
 #pragma unroll
-        for (int b = 0; b < TM; ++b)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                rs_e[a][b][i] = 0u;
-                if constexpr (EPI == EPI_RESID)
-                    rs_e[a][b][i] = resid[(size_t)min(m0 + wm0 + b * 16 + lrow, M - 1) * N + min(nb + i, N - 1)];
-            }
+        for (int b = 0; b < TM; ++b) {
+            rs2[a][b] = uint2{0u, 0u};
+            if constexpr (EPI == EPI_RESID)
+                if (KS == 1 || kg == 0)
+                    rs2[a][b] = *reinterpret_cast<const uint2 *>(
+                        resid + (size_t)min(m0 + wm0 + b * 16 + lrow, M - 1) * N + min(nb, N - 4));
+        }
     }
+    auto rs_at = [&](int a, int b, int i) -> uint16_t {
+        return (uint16_t)((i < 2 ? rs2[a][b].x : rs2[a][b].y) >> (16 * (i & 1)));
+    };
 
     // LNP: the tile's rows of X and gamma/beta are loaded first, the ring's first W tiles go out right
     // behind them, and the LayerNorm runs while those are in flight.  Wave w normalizes rows w,
@@ -619,7 +625,7 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
                 for (int i = 0; i < 4; ++i) {
                     float v = acc[a][b][i];
                     if constexpr (QW) v = v * sc_e[a][i];
-                    o[i] = epi_out<EPI>(v + (bias ? h2f((uint16_t)bs_e[a][i]) : 0.f), (uint16_t)rs_e[a][b][i]);
+                    o[i] = epi_out<EPI>(v + (bias ? h2f((uint16_t)bs_e[a][i]) : 0.f), rs_at(a, b, i));
                 }
                 *reinterpret_cast<uint2 *>(ct + ml * CS + nl) =
                     uint2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
@@ -651,7 +657,7 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
             for (int i = 0; i < 4; ++i) {
                 float v = acc[a][b][i];
                 if constexpr (QW) v = v * sc_e[a][i];
-                o[i] = epi_out<EPI>(v + (bias ? h2f((uint16_t)bs_e[a][i]) : 0.f), (uint16_t)rs_e[a][b][i]);
+                o[i] = epi_out<EPI>(v + (bias ? h2f((uint16_t)bs_e[a][i]) : 0.f), rs_at(a, b, i));
             }
             uint16_t *dst = C + (size_t)m * N + nb;
             if (vec_store && nb + 3 < N) {
@@ -1025,12 +1031,13 @@ void gemm(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const 
 // C = A . W^T (+ bias) followed by the elementwise op `epi` (EPI_GELU, or EPI_RESID: C = resid +
 // product, resid may be C itself), in one launch.  Fused-epilogue kernels exist for the
 // direct-to-LDS configs the prefill picks; returns false (nothing launched) when the picked config
-// has none, for M = 1 (the GEMV), shapes or pointers the MFMA paths cannot take, or a resid that
-// does not share C's 8-byte alignment -- the caller then runs the unfused sequence.
+// has none, for M = 1 (the GEMV), shapes or pointers the MFMA paths cannot take, or (EPI_RESID) C
+// or resid rows that are not 8-byte aligned -- the caller then runs the unfused sequence.
 bool gemm_fused(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const uint16_t *bias, int M, int N,
                 int K, bool qw, int epi, const uint16_t *resid) {
     if (M <= 1 || N <= 0 || K <= 0 || !mfma_ok(A, W, K, qw)) return false;
-    if (epi == EPI_RESID && (!resid || (((uintptr_t)resid ^ (uintptr_t)C) & 7u))) return false;
+    // the residual form reads the residual 4 columns (8 bytes) at a time
+    if (epi == EPI_RESID && (!resid || N % 4 || (((uintptr_t)resid | (uintptr_t)C) & 7u))) return false;
     if (epi != EPI_GELU && epi != EPI_RESID) return false;
     const int c = pick_cfg(M, N, K, qw);
     if (c < 0) return false;

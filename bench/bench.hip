@@ -18,7 +18,8 @@ int gpt2_tune_gemm_fused(gpt2_half *C, const gpt2_half *A, const void *W, const 
 // 2 = fp16 GEMV (gpt2_gemv_fp16), 3 = INT8 GEMV (gpt2_gemv_int8), 4 = causal prefill attention
 // (gpt2_attention_flash: C = att, A = qkv, M = T), 5 = LayerNorm (gpt2_layernorm: C = out, A = x,
 // W = gamma, bias = beta, M rows of K), 6 = the GEMM with the residual add fused (C = C + A.W^T + b,
-// gpt2_tune_gemm_fused epi 2), 7 = residual add (gpt2_add: C += A, M*N elements), 16 + c = the GEMM
+// gpt2_tune_gemm_fused epi 2), 7 = residual add (gpt2_add: C += A, M*N elements), 8 = the GEMM with
+// gelu fused (gpt2_tune_gemm_fused epi 1), 9 = gelu in place (gpt2_gelu, M*N elements), 16 + c = the GEMM
 // on tile config c (gpt2_tune_gemm_run; INT8 weights when Ws is not NULL), for sweeps that mix
 // configs in one step.
 typedef struct {
@@ -41,6 +42,8 @@ static void run_op(const GPT2BenchOp &o) {
         case 5: gpt2_layernorm(o.C, o.A, (const gpt2_half *)o.W, o.bias, o.M, o.K); break;
         case 6: gpt2_tune_gemm_fused(o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K, g2::EPI_RESID, o.C); break;
         case 7: gpt2_add(o.C, o.A, (size_t)o.M * o.N); break;
+        case 8: gpt2_tune_gemm_fused(o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K, g2::EPI_GELU, nullptr); break;
+        case 9: gpt2_gelu(o.C, (size_t)o.M * o.N); break;
         default: gpt2_tune_gemm_run(o.kind - 16, o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K); break;
     }
 }

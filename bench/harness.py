@@ -21,7 +21,8 @@ class GPT2BenchOp(C.Structure):
     """One timed operation (bench.hip): kind 0 fp16 GEMM, 1 INT8 GEMM, 2 fp16 GEMV, 3 INT8 GEMV,
     4 causal prefill attention (C = att, A = qkv, M = T), 5 LayerNorm (C = out, A = x, W = gamma,
     bias = beta, M rows of K), 6 GEMM + residual in place (C += A.W^T + b), 7 residual add (C += A,
-    M*N elements), 16 + c the GEMM on tile config c (INT8 when Ws is set)."""
+    M*N elements), 8 GEMM + gelu, 9 gelu in place (M*N elements), 16 + c the GEMM on tile config c
+    (INT8 when Ws is set)."""
     _fields_ = [("kind", C.c_int), ("C", _vp), ("A", _vp), ("W", _vp), ("Ws", _vp), ("bias", _vp),
                 ("M", C.c_int), ("N", C.c_int), ("K", C.c_int)]
 

@@ -292,7 +292,9 @@ def test_fused_epilogues(pkg, L, kind, M, N, K):
     """The prefill's fused-epilogue GEMMs (forward_cuda.cu:99-105 folded into the GEMM: gelu_new of
     fp16(A.W^T + b), and fp16(resid + fp16(A.W^T + b)) with resid == C in place and in a separate
     buffer) against the oracle's matmul, gelu and add on the same fp16 values, at the trunk shapes,
-    ragged M, and N with and without 8-byte C rows (the staged epilogue).  Bar as above."""
+    ragged M, and N with and without 8-byte C rows (the staged epilogue).  Bar as above.  The residual
+    form needs 8-byte C rows (it reads the residual 4 columns at a time): elsewhere it declines and
+    launches nothing, and the prefill runs the unfused sequence."""
     rng = np.random.default_rng(M * 7 + N + K)
     A = f16v(rng, (M, K), 1.0)
     b = f16v(rng, N, 0.01)
@@ -314,6 +316,9 @@ def test_fused_epilogues(pkg, L, kind, M, N, K):
                                          M, N, K, epi, dR.ptr if epi == 2 else None)
             L.gpt2_sync()
             pkg.check("fused gemm")
+            if epi == 2 and N % 4:
+                assert ran == 0, (kind, M, N, K, epi)
+                continue
             assert ran == 1, (kind, M, N, K, epi)
             got = oracle.f16_to_f32(dC.numpy(np.uint16, (M, N)))
             tol_check(got, want)
