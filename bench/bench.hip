@@ -13,6 +13,8 @@ void gpt2_tune_gemm_run(int cfg, gpt2_half *C, const gpt2_half *A, const void *W
                         const gpt2_half *bias, int M, int N, int K);
 int gpt2_tune_gemm_fused(gpt2_half *C, const gpt2_half *A, const void *W, const float *Ws, const gpt2_half *bias,
                          int M, int N, int K, int epi, const gpt2_half *resid);
+int gpt2_tune_gemm_ln(int cfg, gpt2_half *C, const gpt2_half *X, const gpt2_half *g, const gpt2_half *b, const void *W,
+                      const float *Ws, const gpt2_half *bias, int M, int N, int K, int epi);
 
 // One timed operation: kind 0 = fp16 GEMM (gpt2_matmul_tiled), 1 = INT8 GEMM (gpt2_matmul_int8),
 // 2 = fp16 GEMV (gpt2_gemv_fp16), 3 = INT8 GEMV (gpt2_gemv_int8), 4 = causal prefill attention
@@ -21,7 +23,8 @@ int gpt2_tune_gemm_fused(gpt2_half *C, const gpt2_half *A, const void *W, const 
 // gpt2_tune_gemm_fused epi 2), 7 = residual add (gpt2_add: C += A, M*N elements), 8 = the GEMM with
 // gelu fused (gpt2_tune_gemm_fused epi 1), 9 = gelu in place (gpt2_gelu, M*N elements), 16 + c = the GEMM
 // on tile config c (gpt2_tune_gemm_run; INT8 weights when Ws is not NULL), for sweeps that mix
-// configs in one step.
+// configs in one step, 64 + c = the LayerNorm-panel GEMM on LN config c (gpt2_tune_gemm_ln, K = 768,
+// the bias standing in for gamma and beta: a timing form only).
 typedef struct {
     int kind;
     gpt2_half *C;
@@ -44,7 +47,11 @@ static void run_op(const GPT2BenchOp &o) {
         case 7: gpt2_add(o.C, o.A, (size_t)o.M * o.N); break;
         case 8: gpt2_tune_gemm_fused(o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K, g2::EPI_GELU, nullptr); break;
         case 9: gpt2_gelu(o.C, (size_t)o.M * o.N); break;
-        default: gpt2_tune_gemm_run(o.kind - 16, o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K); break;
+        default:
+            if (o.kind >= 64)   // LayerNorm-panel GEMM on LN config kind - 64; the bias doubles as gamma and beta
+                gpt2_tune_gemm_ln(o.kind - 64, o.C, o.A, o.bias, o.bias, o.W, o.Ws, o.bias, o.M, o.N, o.K, 0);
+            else gpt2_tune_gemm_run(o.kind - 16, o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K);
+            break;
     }
 }
 
