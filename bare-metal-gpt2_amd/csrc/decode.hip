@@ -447,6 +447,25 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             emb_t[i] = a.wte[(size_t)token * PD_E + tid + PD_T * i];
             emb_p[i] = a.wpe[(size_t)pos * PD_E + tid + PD_T * i];
         }
+        // The wave's keys and values of layer l (zero past w1).
+        f16x8 kr[8], vr[8];
+        auto load_kv = [&](int l) {
+            const uint16_t *Kc = a.kv + (size_t)(2 * l) * PD_H * hstride + h * hstride;
+            const uint16_t *Vc = Kc + (size_t)PD_H * hstride;
+            const f16x8 z8 = {};
+            const int jk = w0 + lane;
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                kr[c] = (jk < w1) ? *reinterpret_cast<const f16x8 *>(Kc + (size_t)jk * PD_D + 8 * c) : z8;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int key = w0 + slot + 8 * t;
+                vr[t] = (key < w1) ? *reinterpret_cast<const f16x8 *>(Vc + (size_t)key * PD_D + dg) : z8;
+            }
+        };
+        // Layer 0's keys and values go out before its weight rows, so their latency overlaps the
+        // staging (later layers load theirs while waiting for x).
+        load_kv(0);
         if constexpr (Q8) stage_qkv_q8(ldw, a.layers[0].w[0], h, sp, tid);
         else dma_qkv<LY::RB>(ldw, a.layers[0].w[0], h, sp, wave, lane);
         for (int l = 0; l < GPT2_N_LAYER; ++l) {
@@ -454,19 +473,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             uint16_t *Kc = a.kv + (size_t)(2 * l) * PD_H * hstride + h * hstride;
             uint16_t *Vc = a.kv + (size_t)(2 * l + 1) * PD_H * hstride + h * hstride;
             // ---- before the input arrives: the wave's keys/values, LN1 params, q/k/v scales and biases
-            const f16x8 z8 = {};
-            f16x8 kr[8], vr[8];
-            {
-                const int jk = w0 + lane;
-#pragma unroll
-                for (int c = 0; c < 8; ++c)
-                    kr[c] = (jk < w1) ? *reinterpret_cast<const f16x8 *>(Kc + (size_t)jk * PD_D + 8 * c) : z8;
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const int key = w0 + slot + 8 * t;
-                    vr[t] = (key < w1) ? *reinterpret_cast<const f16x8 *>(Vc + (size_t)key * PD_D + dg) : z8;
-                }
-            }
+            if (l > 0) load_kv(l);
             LNParams lnp;
             load_ln(lnp, ly.ln1_g, ly.ln1_b);
             float rs = 1.f;
