@@ -68,10 +68,11 @@ constexpr int PD_PW = AW_V + KS / 2;
 constexpr int RP = 4, RF = 16, RM = 4;             // rows per GEMV work-group: proj, fc, mlp-proj
 constexpr int PD_NW = PD_E / RP;                   // GEMV work-groups with rows (the rest wait for the head)
 constexpr int RH = (PD_V + PD_G - 1) / PD_G;       // head rows per work-group (the last has fewer)
-constexpr int XR = PD_E / PD_T;                    // words of x each thread polls
+constexpr int XW = PD_E / 2;                       // x words: two fp16 each
+constexpr int XR = (XW + PD_T - 1) / PD_T;         // words of x each thread polls
 static_assert(PD_E % RP == 0 && PD_F % RF == 0 && PD_E / RP == PD_F / RF && RM == RP && PD_NW <= PD_NG,
               "the same GEMV work-groups hold proj, fc and mlp-proj rows");
-static_assert(RF % 2 == 0, "fc rows are exchanged in pairs");
+static_assert(RF % 2 == 0 && RP % 2 == 0, "fc rows and x rows are exchanged in pairs");
 static_assert(QR % 32 == 0, "the q/k/v GEMV takes two 16-row passes at a time");
 static_assert(PD_G == PD_T, "the final argmax gives each thread one work-group's candidate");
 static_assert(PD_S * 4 * 64 >= GPT2_N_CTX, "an attention wave holds at most 64 keys of a full cache");
@@ -81,16 +82,16 @@ static_assert(PD_S * 4 * 64 >= GPT2_N_CTX, "an attention wave holds at most 64 k
 // work-groups on different XCDs were measurably slower to become visible.
 constexpr int LINE = 16;                           // words per 128-byte line
 constexpr int pad_line(int n) { return (n + LINE - 1) / LINE * LINE; }
-constexpr int XS_W = pad_line(RP);                 // x: RP words per GEMV work-group
+constexpr int XS_W = pad_line(RP / 2);             // x: RP/2 words (fp16 pairs) per GEMV work-group
 constexpr int AT_W = pad_line(PD_PW);              // attention: PW words per attention work-group
 constexpr int HD_W = pad_line(RF / 2);             // gelu(fc): RF/2 words (fp16 pairs) per GEMV work-group
-constexpr int LL_X = 0;                            // residual stream: 768 words, one fp16 each
+constexpr int LL_X = 0;                            // residual stream: 384 words, two fp16 each
 constexpr int LL_ATT = LL_X + PD_NW * XS_W;        // attention: NA*PW words, fp32
 constexpr int LL_HID = LL_ATT + PD_NA * AT_W;      // gelu(fc): 1536 words, two fp16 each
 constexpr int LL_CAND = LL_HID + PD_NW * HD_W;     // argmax candidates: one word per work-group
 constexpr int LL_WORDS = LL_CAND + PD_G * LINE;
 // word of element i of each buffer
-__device__ __forceinline__ int x_word(int i) { return (i / RP) * XS_W + i % RP; }
+__device__ __forceinline__ int x_word(int i) { return (i / (RP / 2)) * XS_W + i % (RP / 2); }   // pair i
 __device__ __forceinline__ int at_word(int i) { return (i / PD_PW) * AT_W + i % PD_PW; }
 __device__ __forceinline__ int hd_word(int i) { return (i / (RF / 2)) * HD_W + i % (RF / 2); }
 __device__ __forceinline__ int cand_word(int i) { return i * LINE; }
@@ -417,8 +418,9 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     const size_t hstride = (size_t)a.maxT * PD_D;
 
     auto read_x = [&](uint32_t flag, unsigned long long *dbg = nullptr) {
-        return ll_read<XR>(LX, PD_E, flag, a.err, spin, wflag, x_word,
-                          [&](int i, uint32_t d) { xs[i] = __builtin_bit_cast(f16, (uint16_t)d); }, dbg);
+        return ll_read<XR>(LX, XW, flag, a.err, spin, wflag, x_word, [&](int i, uint32_t d) {
+            reinterpret_cast<uint32_t *>(xs)[i] = d;   // elements 2i, 2i + 1
+        }, dbg);
     };
 
     if (wg < PD_NA) {
@@ -732,7 +734,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 if (lane == 0) xout[k] = __builtin_bit_cast(uint16_t, (f16)(v + xown[k]));
             });
             lds_barrier();
-            if (tid < RP) ll_st(LX + x_word(g * RP + tid), xout[tid], seq(4 * l + 1));
+            if (tid < RP / 2) ll_st(LX + x_word(g * RP / 2 + tid), xout[2 * tid] | (xout[2 * tid + 1] << 16), seq(4 * l + 1));
             mark(4 * l + 1);
             // ---- F: LN2 + fc rows [g*RF, +RF) + gelu, exchanged in pairs
             if (!read_x(seq(4 * l + 1))) return;
@@ -768,7 +770,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 if (lane == 0) xout[k] = __builtin_bit_cast(uint16_t, o);
             });
             lds_barrier();
-            if (tid < RM) ll_st(LX + x_word(g * RM + tid), xout[tid], seq(4 * l + 3));
+            if (tid < RM / 2) ll_st(LX + x_word(g * RM / 2 + tid), xout[2 * tid] | (xout[2 * tid + 1] << 16), seq(4 * l + 3));
             if (next) load_phase(WM, a.layers[l + 1].w[3], a.layers[l + 1].s[3], a.layers[l + 1].b[3], g * RM, wave, lane);
             mark(4 * l + 3);
         }
