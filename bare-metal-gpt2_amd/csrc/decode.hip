@@ -96,6 +96,15 @@ __device__ __forceinline__ int at_word(int i) { return (i / PD_PW) * AT_W + i % 
 __device__ __forceinline__ int hd_word(int i) { return (i / (RF / 2)) * HD_W + i % (RF / 2); }
 __device__ __forceinline__ int cand_word(int i) { return i * LINE; }
 constexpr int PD_SPIN = 1 << 15;                   // default poll rounds before a work-group gives up
+// Hold-offs before a GEMV work-group's polls, in s_memrealtime ticks (10 ns), counted from its own
+// previous store.  A poll issued right after the work-group's own store, or long before the words
+// can arrive, slows the exchanges of the whole step (its loads wait behind the store's write-through
+// and load the memory side while the other work-groups' stores drain).  Measured per token at
+// ctx 512: 178.1 us with none, 165.0 with these three; the attention words arrive >= 4.5 us after
+// the mlp-proj store at any position, x and gelu(fc) ~1.3-1.5 us after the store before them.
+constexpr unsigned PD_HOLD_ATT = 250;              // after the mlp-proj store, before the attention words
+constexpr unsigned PD_HOLD_X = 50;                 // after the proj store, before x
+constexpr unsigned PD_HOLD_HID = 40;               // after the fc store, before gelu(fc)
 // Phase numbers (sequence = epoch*64 + phase): per layer l, 4l attention, 4l+1 x after proj,
 // 4l+2 gelu(fc), 4l+3 x after mlp-proj; 48 head candidates.
 constexpr int PH_CAND = 4 * GPT2_N_LAYER;
@@ -125,6 +134,11 @@ __device__ __forceinline__ uint64_t ll_ld(const uint64_t *p) {
 }
 __device__ __forceinline__ void ll_st(uint64_t *p, uint32_t data, uint32_t flag) {
     __hip_atomic_store(p, ((uint64_t)flag << 32) | data, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Spins (s_sleep) until the 100 MHz real-time counter reaches t; wave-uniform, ends by itself.
+__device__ __forceinline__ void hold_until(unsigned long long t) {
+    while (__builtin_amdgcn_s_memrealtime() < t) __builtin_amdgcn_s_sleep(4);
 }
 
 // Polls elements [0, n) of `base` (R per thread, element tid + 256r at word idx(i); all loads in
@@ -679,9 +693,11 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
         load_phase(WF, a.layers[0].w[2], a.layers[0].s[2], a.layers[0].b[2], g * RF, wave, lane);
         load_ln(lnp, a.layers[0].ln2_g, a.layers[0].ln2_b);
         load_phase(WM, a.layers[0].w[3], a.layers[0].s[3], a.layers[0].b[3], g * RM, wave, lane);
+        unsigned long long t_st = __builtin_amdgcn_s_memrealtime();   // this work-group's last store
         for (int l = 0; l < GPT2_N_LAYER; ++l) {
             // ---- P: combine the attention words, proj rows, + bias + residual
             constexpr int NA = PD_NA * PD_PW;
+            hold_until(t_st + PD_HOLD_ATT);
             if (!ll_read<(NA + PD_T - 1) / PD_T>(LA, NA, seq(4 * l), a.err, spin, wflag, at_word,
                                                  [&](int i, uint32_t d) { part[i] = __uint_as_float(d); }))
                 return;
@@ -735,8 +751,10 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             });
             lds_barrier();
             if (tid < RP / 2) ll_st(LX + x_word(g * RP / 2 + tid), xout[2 * tid] | (xout[2 * tid + 1] << 16), seq(4 * l + 1));
+            t_st = __builtin_amdgcn_s_memrealtime();
             mark(4 * l + 1);
             // ---- F: LN2 + fc rows [g*RF, +RF) + gelu, exchanged in pairs
+            hold_until(t_st + PD_HOLD_X);
             if (!read_x(seq(4 * l + 1))) return;
             mark(64 + 4 * l + 2);
             layernorm768(xn, xs, lnp, lane);
@@ -748,8 +766,10 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             lds_barrier();
             if (tid < RF / 2)
                 ll_st(LHd + hd_word(g * RF / 2 + tid), (uint32_t)hout[2 * tid] | ((uint32_t)hout[2 * tid + 1] << 16), seq(4 * l + 2));
+            t_st = __builtin_amdgcn_s_memrealtime();
             mark(4 * l + 2);
             // ---- M: mlp-proj rows [g*RM, +RM) over gelu(fc), + bias + residual
+            hold_until(t_st + PD_HOLD_HID);
             if (!ll_read<PD_F / 2 / PD_T>(LHd, PD_F / 2, seq(4 * l + 2), a.err, spin, wflag, hd_word,
                                           [&](int i, uint32_t d) {
                                               hs[2 * i] = __builtin_bit_cast(f16, (uint16_t)(d & 0xffff));
@@ -771,6 +791,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             });
             lds_barrier();
             if (tid < RM / 2) ll_st(LX + x_word(g * RM / 2 + tid), xout[2 * tid] | (xout[2 * tid + 1] << 16), seq(4 * l + 3));
+            t_st = __builtin_amdgcn_s_memrealtime();
             if (next) load_phase(WM, a.layers[l + 1].w[3], a.layers[l + 1].s[3], a.layers[l + 1].b[3], g * RM, wave, lane);
             mark(4 * l + 3);
         }
