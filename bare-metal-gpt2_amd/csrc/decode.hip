@@ -168,7 +168,7 @@ __device__ bool ll_read(const uint64_t *base, int n, uint32_t flag, int *err, in
             bad = true;
             break;
         }
-        __builtin_amdgcn_s_sleep(2);
+        __builtin_amdgcn_s_sleep(1);   // 64 clocks between rounds (measured: 1 beats 0, 2, 4 and 8)
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int i = threadIdx.x + PD_T * r;
