@@ -100,11 +100,11 @@ constexpr int PD_SPIN = 1 << 15;                   // default poll rounds before
 // previous store.  A poll issued right after the work-group's own store, or long before the words
 // can arrive, slows the exchanges of the whole step (its loads wait behind the store's write-through
 // and load the memory side while the other work-groups' stores drain).  Measured per token at
-// ctx 512: 178.1 us with none, 165.0 with these three; the attention words arrive >= 4.5 us after
+// ctx 512: 178.1 us with none, ~164 with these three; the attention words arrive >= 4.5 us after
 // the mlp-proj store at any position, x and gelu(fc) ~1.3-1.5 us after the store before them.
 constexpr unsigned PD_HOLD_ATT = 250;              // after the mlp-proj store, before the attention words
-constexpr unsigned PD_HOLD_X = 50;                 // after the proj store, before x
-constexpr unsigned PD_HOLD_HID = 40;               // after the fc store, before gelu(fc)
+constexpr unsigned PD_HOLD_X = 60;                 // after the proj store, before x
+constexpr unsigned PD_HOLD_HID = 50;               // after the fc store, before gelu(fc)
 // Phase numbers (sequence = epoch*64 + phase): per layer l, 4l attention, 4l+1 x after proj,
 // 4l+2 gelu(fc), 4l+3 x after mlp-proj; 48 head candidates.
 constexpr int PH_CAND = 4 * GPT2_N_LAYER;
