@@ -168,6 +168,8 @@ SIGNATURES = {
     "gpt2_tune_prefill_persistent": (None, [_i]),
     "gpt2_tune_prefill_spin": (None, [_i]),
     "gpt2_prefill_status": (_i, []),
+    "gpt2_test_dmalloc_calls": (C.c_long, []),
+    "gpt2_test_mem_free": (C.c_longlong, []),
     "gpt2_tune_prefill_trace": (_i, [_vp, _i, _i]),
     "gpt2_tune_gemm_pick_q": (_i, [_i, _i, _i, _i]),
     "gpt2_tune_gemm_fits": (_i, [_i, _i]),

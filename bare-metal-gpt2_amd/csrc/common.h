@@ -29,6 +29,14 @@ enum { E_ARG = 1000, E_ALIGN = 1001, E_FORMAT = 1002, E_CAPACITY = 1003, E_STATE
 // Check the launch that was just enqueued.
 void check_launch(const char *what);
 
+// Resolves (once per device) the device address of gpt2_forward_noalloc's static scratch on the
+// current device; gpt2_set_stream calls it so that a caller who captures the no-allocation forward
+// into a graph has it resolved before the capture begins.
+void noalloc_prepare();
+// Synchronizing calls (gpt2_sync) ask this after the stream drains: nonzero when a persistent
+// prefill launched since the last check gave up waiting (its sticky error word, cleared here).
+int prefill_persist_take_error();
+
 // A decode step reads (token, pos) from immediates or, under graph replay, from a small
 // device-resident state {token, pos}.
 struct StepArg {

@@ -105,30 +105,37 @@ extern "C" size_t gpt2_bind_weights(GPT2Weights *w, float *body) {
     return (size_t)(c - body);
 }
 
+// A loader's diagnostic on stderr (the return code carries the reason to the caller).
+static int load_reject(const char *loader, const char *path, const char *why, int code) {
+    fprintf(stderr, "%s: %s: %s\n", loader, path, why);
+    return code;
+}
+
 extern "C" int gpt2_load_weights(const char *path, GPT2Weights *w) {
+    static const char *me = "gpt2_load_weights";
     memset(w, 0, sizeof(*w));
     FILE *f = fopen(path, "rb");
-    if (!f) { fprintf(stderr, "[weights] cannot open %s\n", path); return 1; }
-    int32_t hdr[16];
-    if (fread(hdr, 4, 16, f) != 16) { fclose(f); fprintf(stderr, "[weights] short header\n"); return 2; }
-    if (hdr[0] != kMagicW || hdr[1] != 1) { fclose(f); fprintf(stderr, "[weights] bad magic/version\n"); return 3; }
-    if (hdr[2] != GPT2_N_LAYER || hdr[3] != GPT2_N_HEAD || hdr[4] != GPT2_N_EMBD || hdr[5] != GPT2_VOCAB ||
-        hdr[6] != GPT2_N_CTX || hdr[7] != GPT2_FFN_DIM || hdr[8] != GPT2_QKV_DIM) {
+    if (!f) return load_reject(me, path, "cannot be opened for reading", 1);
+    int32_t head[16];
+    const bool whole = fread(head, 4, 16, f) == 16;
+    if (!whole) { fclose(f); return load_reject(me, path, "the file ends inside its 64-byte header", 2); }
+    if (head[0] != kMagicW || head[1] != 1) { fclose(f); return load_reject(me, path, "not a 'GPT2' version 1 file", 3); }
+    const int32_t dims[7] = {GPT2_N_LAYER, GPT2_N_HEAD, GPT2_N_EMBD, GPT2_VOCAB, GPT2_N_CTX, GPT2_FFN_DIM, GPT2_QKV_DIM};
+    if (memcmp(head + 2, dims, sizeof dims) != 0) {
         fclose(f);
-        fprintf(stderr, "[weights] dims mismatch\n");
-        return 4;
+        return load_reject(me, path, "its model dimensions are not GPT-2-124M's", 4);
     }
-    if (hdr[9] != 0) { fclose(f); fprintf(stderr, "[weights] dtype != fp32\n"); return 5; }
+    if (head[9] != 0) { fclose(f); return load_reject(me, path, "its tensors are not stored as fp32", 5); }
     const size_t n = (size_t)GPT2_TOTAL_PARAMS;
     float *body = (float *)malloc(n * sizeof(float));
     if (!body) { fclose(f); return 6; }
     const size_t got = fread(body, sizeof(float), n, f);
-    const long cur = ftell(f);
+    const long at = ftell(f);
     fseek(f, 0, SEEK_END);
-    const long extra = ftell(f) - cur;
+    const long past_end = ftell(f) - at;
     fclose(f);
-    if (got != n) { free(body); fprintf(stderr, "[weights] short body\n"); return 7; }
-    if (extra != 0) { free(body); fprintf(stderr, "[weights] %ld trailing bytes\n", extra); return 8; }
+    if (got != n) { free(body); return load_reject(me, path, "the file ends inside the tensor data", 7); }
+    if (past_end != 0) { free(body); return load_reject(me, path, "bytes follow the last tensor", 8); }
     if (gpt2_bind_weights(w, body) != n) { free(body); memset(w, 0, sizeof(*w)); return 9; }
     return 0;
 }
@@ -357,6 +364,8 @@ static uint16_t *scratch_ptr() {
     }
     return g_scratch_ptr[dev];
 }
+
+void g2::noalloc_prepare() { (void)scratch_ptr(); }
 
 extern "C" void gpt2_forward_noalloc(const GPT2Backend *be, const GPT2WeightsGPU *w, const int *d_ids, int T,
                                      GPT2CapsGPU *caps) {
@@ -687,27 +696,33 @@ extern "C" void gpt2_decode_graph_destroy(GPT2DecodeGraph *g) {
 
 // ============================================================================ INT8 weights
 namespace {
+// The 49 quantizable matrices in file order: the tied head wte, then per layer qkv, attn_proj, fc,
+// proj (row count N = output features, column count K = input features).
 const int kNQ = 1 + 4 * GPT2_N_LAYER;
 
-struct QShape { int N, K; };
+struct MatDims {
+    int rows, cols;
+    size_t elems() const { return (size_t)rows * cols; }
+};
 
-void q_shapes(QShape *sh) {
-    sh[0] = {GPT2_VOCAB, GPT2_N_EMBD};
-    for (int L = 0; L < GPT2_N_LAYER; ++L) {
-        sh[1 + 4 * L + 0] = {GPT2_QKV_DIM, GPT2_N_EMBD};
-        sh[1 + 4 * L + 1] = {GPT2_N_EMBD, GPT2_N_EMBD};
-        sh[1 + 4 * L + 2] = {GPT2_FFN_DIM, GPT2_N_EMBD};
-        sh[1 + 4 * L + 3] = {GPT2_N_EMBD, GPT2_FFN_DIM};
+MatDims matrix_dims(int i) {
+    if (i == 0) return {GPT2_VOCAB, GPT2_N_EMBD};
+    switch ((i - 1) % 4) {
+        case 0: return {GPT2_QKV_DIM, GPT2_N_EMBD};
+        case 1: return {GPT2_N_EMBD, GPT2_N_EMBD};
+        case 2: return {GPT2_FFN_DIM, GPT2_N_EMBD};
+        default: return {GPT2_N_EMBD, GPT2_FFN_DIM};
     }
 }
 
-void q_slots(GPT2QWeightsGPU *q, GPT2QW **dst) {
-    dst[0] = &q->wte;
-    for (int L = 0; L < GPT2_N_LAYER; ++L) {
-        dst[1 + 4 * L + 0] = &q->layers[L].qkv_w;
-        dst[1 + 4 * L + 1] = &q->layers[L].attn_proj_w;
-        dst[1 + 4 * L + 2] = &q->layers[L].fc_w;
-        dst[1 + 4 * L + 3] = &q->layers[L].proj_w;
+GPT2QW *qw_slot(GPT2QWeightsGPU *q, int i) {
+    if (i == 0) return &q->wte;
+    GPT2QLayerGPU &l = q->layers[(i - 1) / 4];
+    switch ((i - 1) % 4) {
+        case 0: return &l.qkv_w;
+        case 1: return &l.attn_proj_w;
+        case 2: return &l.fc_w;
+        default: return &l.proj_w;
     }
 }
 
@@ -722,26 +737,32 @@ const gpt2_half *fp16_tensor(const GPT2WeightsGPU *w, int i) {
     }
 }
 
-// Point the GPT2QW views into the arenas; flag 0 leaves q = NULL (fp16 fallback for that tensor).
-void q_attach(GPT2QWeightsGPU *q, const int *flag) {
-    QShape sh[kNQ];
-    q_shapes(sh);
-    GPT2QW *dst[kNQ];
-    q_slots(q, dst);
-    size_t oq = 0, os = 0, kept = 0;
+// Arena sizes of the quantized matrices (quantized[i] != 0): int8 codes and fp32 row scales.
+void arena_sizes(const int *quantized, size_t *codes, size_t *scales) {
+    *codes = *scales = 0;
+    for (int i = 0; i < kNQ; ++i)
+        if (quantized[i]) { *codes += matrix_dims(i).elems(); *scales += matrix_dims(i).rows; }
+}
+
+// Points each GPT2QW view into the arenas, matrix after matrix; an unquantized matrix gets q = s =
+// NULL (it stays fp16) and counts its fp16 bytes in the per-step stream.
+void q_attach(GPT2QWeightsGPU *q, const int *quantized) {
+    size_t code_at = 0, scale_at = 0, fp16_elems = 0;
     for (int i = 0; i < kNQ; ++i) {
-        if (!flag[i]) {
-            dst[i]->q = nullptr;
-            dst[i]->s = nullptr;
-            kept += (size_t)sh[i].N * sh[i].K;
+        GPT2QW *v = qw_slot(q, i);
+        const MatDims d = matrix_dims(i);
+        if (!quantized[i]) {
+            v->q = nullptr;
+            v->s = nullptr;
+            fp16_elems += d.elems();
             continue;
         }
-        dst[i]->q = q->qdata + oq;
-        dst[i]->s = q->sdata + os;
-        oq += (size_t)sh[i].N * sh[i].K;
-        os += sh[i].N;
+        v->q = q->qdata + code_at;
+        v->s = q->sdata + scale_at;
+        code_at += d.elems();
+        scale_at += d.rows;
     }
-    q->streamed_bytes = q->nq + q->ns * 4 + kept * 2;
+    q->streamed_bytes = q->nq + q->ns * 4 + fp16_elems * 2;
 }
 }  // namespace
 
@@ -756,92 +777,88 @@ extern "C" void gpt2_quant_free(GPT2QWeightsGPU *q) {
 extern "C" int gpt2_quant_build(GPT2WeightsGPU *gpu, GPT2QWeightsGPU *q, const int *keep) {
     memset(q, 0, sizeof(*q));
     if (!gpu || !gpu->data) { arg_fail("gpt2_quant_build: no fp16 weights"); return 1; }
-    int flag[kNQ];
-    for (int i = 0; i < kNQ; ++i) flag[i] = keep ? !keep[i] : (i != 0);
-    QShape sh[kNQ];
-    q_shapes(sh);
-    for (int i = 0; i < kNQ; ++i)
-        if (flag[i]) { q->nq += (size_t)sh[i].N * sh[i].K; q->ns += sh[i].N; }
+    int quantized[kNQ];
+    for (int i = 0; i < kNQ; ++i) quantized[i] = keep ? !keep[i] : (i != 0);
+    arena_sizes(quantized, &q->nq, &q->ns);
     q->qdata = (int8_t *)gpt2_dmalloc(q->nq ? q->nq : 1);
     q->sdata = (float *)gpt2_dmalloc((q->ns ? q->ns : 1) * 4);
     if (!q->qdata || !q->sdata) { gpt2_quant_free(q); return 1; }
-    q_attach(q, flag);
-    GPT2QW *dst[kNQ];
-    q_slots(q, dst);
-    for (int i = 0; i < kNQ; ++i)
-        if (flag[i]) gpt2_quantize_rows((int8_t *)dst[i]->q, (float *)dst[i]->s, fp16_tensor(gpu, i), sh[i].N, sh[i].K);
+    q_attach(q, quantized);
+    for (int i = 0; i < kNQ; ++i) {
+        if (!quantized[i]) continue;
+        GPT2QW *v = qw_slot(q, i);
+        gpt2_quantize_rows((int8_t *)v->q, (float *)v->s, fp16_tensor(gpu, i), matrix_dims(i).rows, matrix_dims(i).cols);
+    }
     if (gpt2_sync()) { gpt2_quant_free(q); return 1; }
     gpu->q = q;
     return 0;
 }
 
 extern "C" int gpt2_quant_load_upload(const char *path, GPT2WeightsGPU *gpu, GPT2QWeightsGPU *q) {
+    static const char *me = "gpt2_quant_load_upload";
     memset(q, 0, sizeof(*q));
     FILE *f = fopen(path, "rb");
-    if (!f) { fprintf(stderr, "[quant] cannot open %s\n", path); return 1; }
-    int32_t hdr[16];
-    int flag[kNQ];
-    auto fail = [&](const char *why) { fprintf(stderr, "[quant] %s\n", why); fclose(f); return 1; };
-    if (fread(hdr, 4, 16, f) != 16) return fail("short header");
-    if (hdr[0] != kMagicQ) return fail("bad magic");
-    if (hdr[1] != 2) return fail("version != 2");
-    if (hdr[2] != GPT2_N_LAYER || hdr[3] != GPT2_N_EMBD || hdr[4] != GPT2_VOCAB || hdr[5] != GPT2_FFN_DIM ||
-        hdr[6] != GPT2_QKV_DIM || hdr[7] != kNQ)
-        return fail("dim mismatch");
-    if (fread(flag, 4, kNQ, f) != (size_t)kNQ) return fail("short flags");
-    QShape sh[kNQ];
-    q_shapes(sh);
-    for (int i = 0; i < kNQ; ++i)
-        if (flag[i]) { q->nq += (size_t)sh[i].N * sh[i].K; q->ns += sh[i].N; }
-    std::vector<int8_t> hq(q->nq ? q->nq : 1);
-    std::vector<float> hs(q->ns ? q->ns : 1);
-    size_t oq = 0, os = 0;
+    if (!f) return load_reject(me, path, "cannot be opened for reading", 1);
+    auto reject = [&](const char *why) { fclose(f); return load_reject(me, path, why, 1); };
+    int32_t head[16];
+    if (fread(head, 4, 16, f) != 16) return reject("the file ends inside its 64-byte header");
+    if (head[0] != kMagicQ || head[1] != 2) return reject("not a 'GPQ8' version 2 file");
+    const int32_t dims[6] = {GPT2_N_LAYER, GPT2_N_EMBD, GPT2_VOCAB, GPT2_FFN_DIM, GPT2_QKV_DIM, kNQ};
+    if (memcmp(head + 2, dims, sizeof dims) != 0) return reject("its model dimensions are not GPT-2-124M's");
+    int quantized[kNQ];
+    if (fread(quantized, 4, kNQ, f) != (size_t)kNQ) return reject("the file ends inside its per-matrix flags");
+    for (int i = 0; i < kNQ; ++i) quantized[i] = quantized[i] != 0;
+    arena_sizes(quantized, &q->nq, &q->ns);
+    // the file holds, per quantized matrix in order, its codes then its row scales; both go to host
+    // staging arenas laid out as the device arenas are
+    std::vector<int8_t> codes(q->nq ? q->nq : 1);
+    std::vector<float> scales(q->ns ? q->ns : 1);
+    size_t code_at = 0, scale_at = 0;
     for (int i = 0; i < kNQ; ++i) {
-        if (!flag[i]) continue;
-        const size_t n = (size_t)sh[i].N * sh[i].K;
-        if (fread(hq.data() + oq, 1, n, f) != n) return fail("short q");
-        if (fread(hs.data() + os, 4, sh[i].N, f) != (size_t)sh[i].N) return fail("short s");
-        oq += n;
-        os += sh[i].N;
+        if (!quantized[i]) continue;
+        const MatDims d = matrix_dims(i);
+        if (fread(codes.data() + code_at, 1, d.elems(), f) != d.elems()) return reject("the file ends inside a matrix's codes");
+        if (fread(scales.data() + scale_at, 4, d.rows, f) != (size_t)d.rows) return reject("the file ends inside a matrix's scales");
+        code_at += d.elems();
+        scale_at += d.rows;
     }
-    const long cur = ftell(f);
+    const long at = ftell(f);
     fseek(f, 0, SEEK_END);
-    const long extra = ftell(f) - cur;
+    const long past_end = ftell(f) - at;
     fclose(f);
-    if (extra != 0) { fprintf(stderr, "[quant] %ld trailing bytes\n", extra); return 1; }
+    if (past_end != 0) return load_reject(me, path, "bytes follow the last matrix", 1);
     q->qdata = (int8_t *)gpt2_dmalloc(q->nq ? q->nq : 1);
     q->sdata = (float *)gpt2_dmalloc((q->ns ? q->ns : 1) * 4);
     if (!q->qdata || !q->sdata) { gpt2_quant_free(q); return 1; }
-    if (gpt2_h2d(q->qdata, hq.data(), q->nq) || gpt2_h2d(q->sdata, hs.data(), q->ns * 4)) { gpt2_quant_free(q); return 1; }
-    int fl[kNQ];
-    for (int i = 0; i < kNQ; ++i) fl[i] = flag[i] != 0;
-    q_attach(q, fl);
+    if (gpt2_h2d(q->qdata, codes.data(), q->nq) || gpt2_h2d(q->sdata, scales.data(), q->ns * 4)) {
+        gpt2_quant_free(q);
+        return 1;
+    }
+    q_attach(q, quantized);
     if (gpu) gpu->q = q;
     return 0;
 }
 
 extern "C" int gpt2_quant_write_file(const char *path, const GPT2QWeightsGPU *q, const int *keep) {
     if (!q || !path) return 1;
-    int flag[kNQ];
-    QShape sh[kNQ];
-    q_shapes(sh);
-    GPT2QW *dst[kNQ];
-    q_slots(const_cast<GPT2QWeightsGPU *>(q), dst);
-    for (int i = 0; i < kNQ; ++i) flag[i] = dst[i]->q != nullptr;
+    GPT2QWeightsGPU *views = const_cast<GPT2QWeightsGPU *>(q);
+    int quantized[kNQ];
+    for (int i = 0; i < kNQ; ++i) quantized[i] = qw_slot(views, i)->q != nullptr;
     if (keep)
         for (int i = 0; i < kNQ; ++i)
-            if (keep[i] && flag[i]) return 1;   // asked to keep a tensor that is quantized
+            if (keep[i] && quantized[i]) return 1;   // asked to keep a tensor that is quantized
     FILE *f = fopen(path, "wb");
     if (!f) return 1;
-    int32_t hdr[16] = {kMagicQ, 2, GPT2_N_LAYER, GPT2_N_EMBD, GPT2_VOCAB, GPT2_FFN_DIM, GPT2_QKV_DIM, kNQ};
-    bool ok = fwrite(hdr, 4, 16, f) == 16 && fwrite(flag, 4, kNQ, f) == (size_t)kNQ;
+    int32_t head[16] = {kMagicQ, 2, GPT2_N_LAYER, GPT2_N_EMBD, GPT2_VOCAB, GPT2_FFN_DIM, GPT2_QKV_DIM, kNQ};
+    bool ok = fwrite(head, 4, 16, f) == 16 && fwrite(quantized, 4, kNQ, f) == (size_t)kNQ;
     for (int i = 0; ok && i < kNQ; ++i) {
-        if (!flag[i]) continue;
-        const size_t n = (size_t)sh[i].N * sh[i].K;
-        std::vector<int8_t> hq(n);
-        std::vector<float> hs(sh[i].N);
-        ok = !gpt2_d2h(hq.data(), dst[i]->q, n) && !gpt2_d2h(hs.data(), dst[i]->s, (size_t)sh[i].N * 4) &&
-             fwrite(hq.data(), 1, n, f) == n && fwrite(hs.data(), 4, sh[i].N, f) == (size_t)sh[i].N;
+        if (!quantized[i]) continue;
+        const MatDims d = matrix_dims(i);
+        const GPT2QW *v = qw_slot(views, i);
+        std::vector<int8_t> codes(d.elems());
+        std::vector<float> scales(d.rows);
+        ok = !gpt2_d2h(codes.data(), v->q, d.elems()) && !gpt2_d2h(scales.data(), v->s, (size_t)d.rows * 4) &&
+             fwrite(codes.data(), 1, d.elems(), f) == d.elems() && fwrite(scales.data(), 4, d.rows, f) == (size_t)d.rows;
     }
     return (fclose(f) == 0 && ok) ? 0 : 1;
 }

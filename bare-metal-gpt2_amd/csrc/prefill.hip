@@ -460,6 +460,9 @@ int g_spin = PF_SPIN;
 uint64_t *g_trace = nullptr;   // per-task trace buffer (test/tuning hook) and its capacity in tasks
 int g_trace_cap = 0;
 
+// One arena per process, on the device of the last launch: its counters, ticket and activation
+// buffers serve one launch at a time, so a launch on another stream waits its turn (prefill_persist
+// falls back to the launch sequence while the previous stream's launch may still run).
 struct Arena {
     int dev = -1, maxT = 0;
     uint16_t *act = nullptr;     // all layer buffers
@@ -468,8 +471,23 @@ struct Arena {
     int taskT = 0, ntasks = 0, cap_tasks = 0;
     int grid = 0;
     bool fits = false;
+    hipStream_t last_stream = nullptr;   // the stream of the last launch
+    bool unchecked = false;              // launched since the sticky error word was last read
 };
 Arena g_arena;
+
+// Frees the arena's buffers on their own device (made current for the frees, then restored).
+void arena_release(Arena &A) {
+    if (A.dev < 0) return;
+    int cur = 0;
+    const bool have = hipGetDevice(&cur) == hipSuccess;
+    if (have && cur != A.dev) (void)hipSetDevice(A.dev);
+    gpt2_dfree(A.act);
+    gpt2_dfree(A.cnt);
+    gpt2_dfree(A.tasks);
+    if (have && cur != A.dev) (void)hipSetDevice(cur);
+    A = Arena();
+}
 
 // Task list in dependency order: embedding per row block, then per layer QKV tiles, attention
 // blocks (lightest first: their inputs are ready first), attn-proj, fc and mlp-proj tiles, each by
@@ -501,7 +519,7 @@ bool arena_ready(int T, bool q8) {
     if (hipGetDevice(&dev) != hipSuccess) return false;
     Arena &A = g_arena;
     if (A.dev != dev) {   // a new device: start over (the old buffers belong to another device)
-        A = Arena();
+        arena_release(A);
         A.dev = dev;
         int ncu = 0, per = 0, per8 = 0;
         if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
@@ -558,11 +576,19 @@ const uint16_t *prefill_persist(const GPT2Backend *be, const GPT2WeightsGPU *w, 
     }
     const bool q8 = q_ok && nq == GPT2_N_LAYER;
     if (q_ok && nq != 0 && nq != GPT2_N_LAYER) return nullptr;
-    if (!arena_ready(T, q8)) {
-        gpt2_last_error();   // fall back quietly to the multi-launch prefill
+    Arena &A = g_arena;
+    // one launch at a time: on another stream, only once the previous stream has drained
+    if (A.last_stream && A.last_stream != stream() && hipStreamQuery(A.last_stream) != hipSuccess) {
+        (void)hipGetLastError();   // hipErrorNotReady is not an error of the caller's
         return nullptr;
     }
-    Arena &A = g_arena;
+    // fall back quietly to the multi-launch prefill when the arena cannot be set up; an error the
+    // caller has not read yet stays recorded
+    const int pending = gpt2_last_error();
+    const bool ready = arena_ready(T, q8);
+    (void)gpt2_last_error();
+    if (pending) set_error(pending, "an earlier call (recorded before the persistent prefill's set-up)");
+    if (!ready) return nullptr;
     PFArgs a;
     memset(&a, 0, sizeof(a));
     const size_t t = (size_t)T, E = GPT2_N_EMBD;
@@ -616,6 +642,8 @@ const uint16_t *prefill_persist(const GPT2Backend *be, const GPT2WeightsGPU *w, 
     if (q8) hipLaunchKernelGGL(k_prefill_persist<true>, dim3(A.grid), dim3(PF_T), 0, stream(), a);
     else hipLaunchKernelGGL(k_prefill_persist<false>, dim3(A.grid), dim3(PF_T), 0, stream(), a);
     check_launch("k_prefill_persist");
+    A.last_stream = stream();
+    A.unchecked = true;
     if (embed_out) *embed_out = x;
     return x + t * E * GPT2_N_LAYER;
 }
@@ -641,15 +669,25 @@ extern "C" int gpt2_tune_prefill_trace(unsigned long long *buf, int cap, int T) 
     return T >= 1 && T <= GPT2_N_CTX ? (int)g2::build_tasks(T).size() : 0;
 }
 // Synchronizes and returns (then clears) the persistent prefill's sticky error word: nonzero when a
-// launch since the last call gave up waiting (its results are void).
+// launch since the last call gave up waiting (its results are void).  gpt2_sync makes the same check
+// and records the error (gpt2_last_error) when the word is set.
 extern "C" int gpt2_prefill_status(void) {
     if (!g2::g_arena.cnt) return 0;
     uint32_t e = 0;
-    if (hipStreamSynchronize(g2::stream()) != hipSuccess) return -1;
+    hipStream_t s = g2::g_arena.last_stream ? g2::g_arena.last_stream : g2::stream();
+    if (hipStreamSynchronize(s) != hipSuccess) return -1;
     if (hipMemcpy(&e, g2::g_arena.cnt + g2::PF_NCNT + 3, sizeof(e), hipMemcpyDeviceToHost) != hipSuccess) return -1;
     if (e) {
         const uint32_t z = 0;
         hipMemcpy(g2::g_arena.cnt + g2::PF_NCNT + 3, &z, sizeof(z), hipMemcpyHostToDevice);
     }
+    g2::g_arena.unchecked = false;
     return (int)e;
+}
+
+int g2::prefill_persist_take_error() {
+    if (!g_arena.unchecked || !g_arena.cnt) return 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev != g_arena.dev) return 0;
+    return gpt2_prefill_status() > 0;
 }

@@ -31,7 +31,12 @@ void check_launch(const char *what) {
 
 using namespace g2;
 
-extern "C" void gpt2_set_stream(void *s) { g_stream = (hipStream_t)s; }
+// A non-null stream is what graph capture needs, so selecting one also resolves the no-allocation
+// forward's static scratch address for the current device (outside any capture that follows).
+extern "C" void gpt2_set_stream(void *s) {
+    g_stream = (hipStream_t)s;
+    if (s) noalloc_prepare();
+}
 extern "C" void *gpt2_get_stream(void) { return (void *)g_stream; }
 
 extern "C" int gpt2_last_error(void) {
@@ -53,7 +58,20 @@ extern "C" const char *gpt2_error_string(int code) {
     return buf;
 }
 
+// Every device allocation of the library goes through gpt2_dmalloc; the count is a test hook
+// (gpt2_test_dmalloc_calls) for entry points that promise to allocate nothing.
+static std::atomic<long> g_dmalloc_calls{0};
+
+extern "C" long gpt2_test_dmalloc_calls(void) { return g_dmalloc_calls.load(); }
+
+// Test hook: free device memory on the current device (hipMemGetInfo), or -1 on failure.
+extern "C" long long gpt2_test_mem_free(void) {
+    size_t f = 0, t = 0;
+    return hipMemGetInfo(&f, &t) == hipSuccess ? (long long)f : -1;
+}
+
 extern "C" void *gpt2_dmalloc(size_t bytes) {
+    g_dmalloc_calls.fetch_add(1);
     void *p = nullptr;
     hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
     if (e != hipSuccess) {
@@ -99,6 +117,10 @@ extern "C" int gpt2_memset(void *d, int v, size_t n) {
 extern "C" int gpt2_sync(void) {
     hipError_t e = hipStreamSynchronize(g_stream);
     if (e != hipSuccess) { set_error((int)e, "sync"); return (int)e; }
+    if (prefill_persist_take_error()) {
+        set_error(E_STATE, "persistent prefill gave up waiting on a dependency (its outputs are void)");
+        return E_STATE;
+    }
     return 0;
 }
 

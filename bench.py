@@ -105,6 +105,18 @@ class Bench:
             raise RuntimeError(f"gpt2_bench_ops rc={rc}")
         return ms.value, (list(per) if per_op else None)
 
+    def run_steps(self, ops, warmup, iters):
+        """Per-round times (ms) of `iters` rounds of ops, each between its own pair of events on the
+        launch stream, and the first-to-last total."""
+        arr = (self.harness.GPT2BenchOp * len(ops))(*ops)
+        per = (C.c_float * iters)()
+        tot = C.c_float()
+        rc = self.H.gpt2_bench_ops_steps(arr, len(ops), warmup, iters, per, C.byref(tot))
+        if rc:
+            self.pkg.check("gpt2_bench_ops_steps")
+            raise RuntimeError(f"gpt2_bench_ops_steps rc={rc}")
+        return list(per), tot.value
+
     def run_ops_graph(self, ops, warmup, iters):
         """Mean ms per round when one round is captured once as a hipGraph and replayed."""
         arr = (self.harness.GPT2BenchOp * len(ops))(*ops)
@@ -135,7 +147,15 @@ def bench_gemm_set(B, steps, warmup):
             A = Xf if K == 3072 else X
             ops.append(B.op(0, outs[name].ptr, A.ptr, W.ptr, None, b.ptr, M_PREFILL, N, K))
     flops_step = sum(2.0 * M_PREFILL * N * K for _, N, K in GEMM_SET) * N_LAYER
-    ms_step, _ = B.run_ops(ops, warmup, steps)
+    per_ms, total_ms = B.run_steps(ops, warmup, steps)
+    ms_step = total_ms / steps
+    tf = lambda ms: round(flops_step / (ms * 1e-3) / 1e12, 2)
+    step_stats = {"mean_ms": round(ms_step, 5), "median_ms": round(float(np.median(per_ms)), 5),
+                  "min_ms": round(min(per_ms), 5), "max_ms": round(max(per_ms), 5), "n": steps,
+                  "tflops_median": tf(float(np.median(per_ms))), "tflops_at_min_max_ms": [tf(min(per_ms)), tf(max(per_ms))],
+                  "timing": "one hipEvent pair per step on the launch stream (steps share their boundary events); "
+                            "ms_per_step and value use the mean"}
+    clock = sustained_clock(B, ops)
     ms_graph = B.run_ops_graph(ops, warmup, steps)
     # Per-kernel launch durations for the roofline, under the step's own conditions: each shape's
     # 12 layer GEMMs (distinct weights, so the weights are not L2-resident) back to back.
@@ -155,13 +175,57 @@ def bench_gemm_set(B, steps, warmup):
         c["launches"] += 1
     dom = max(by_cfg.items(), key=lambda kv: kv[1]["ms"])
     d = dom[1]
-    achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
+    flops_launch = d["flops"] / d["launches"]
+    live_us = d["ms"] / d["launches"] * 1e3
+    achieved_live = flops_launch / (live_us * 1e-6) / 1e12
+    # Primary time: the rocprofv3 kernel duration of this kernel in the committed trace of the same
+    # workload (profiles/gemm_prefill_p512_kernel_trace.json); the hipEvent figure of this run beside it.
+    prof = rocprof_kernel_time(dom[0])
+    if prof:
+        achieved = flops_launch / (prof["mean_us"] * 1e-6) / 1e12
+        src = {"time_source": "rocprofv3 kernel duration (mean over dispatches)", "rocprof_mean_us": prof["mean_us"],
+               "rocprof_median_us": prof["median_us"], "rocprof_dispatches": prof["dispatches"],
+               "rocprof_profile": prof["source"]}
+    else:
+        achieved = achieved_live
+        src = {"time_source": "hipEvents in this run (no committed rocprofv3 trace covers this kernel config)"}
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": None,
-                "kernel": dom[0], "avg_launch_us": round(d["ms"] / d["launches"] * 1e3, 3),
-                "flops_per_launch": d["flops"] / d["launches"]}
+                "kernel": dom[0], "flops_per_launch": flops_launch, **src,
+                "avg_launch_us": round(live_us, 3), "achieved_live": round(achieved_live, 2),
+                "frac_live": round(achieved_live / PEAK_FP16_TFLOPS, 4),
+                "live_method": "hipEvents around 12 back-to-back launches of this shape (distinct weights), this run"}
     roofline.update(measured_traffic(dom[0], [x for x in shapes if x["kernel"] == dom[0]]))
-    return flops_step, ms_step, shapes, roofline, ms_graph
+    return flops_step, ms_step, shapes, roofline, ms_graph, step_stats, clock
+
+
+def cfg_tag(cfg_name):
+    """The kernel's template name (as rocprofv3 prints it) of a GEMM tile config name."""
+    import re
+    m = re.fullmatch(r"dl_bn(\d+)_bm(\d+)_w(\d+)x(\d+)_s(\d+)(?:_k(\d+))?(?:_u(\d+))?", cfg_name)
+    if m:
+        g = m.groups()
+        return "k_gemm_dl<{}, {}, {}, {}, {}, false, {}, {}, 0>".format(*g[:5], g[5] or 1, g[6] or 1)
+    m = re.fullmatch(r"bn(\d+)_bm(\d+)_bk(\d+)_w(\d+)x(\d+)_d(\d+)", cfg_name)
+    if m:
+        return "k_gemm_mfma<{}, {}, {}, {}, {}, false, {}, false>".format(*m.groups())
+    return None
+
+
+def rocprof_kernel_time(cfg_name):
+    """Mean / median kernel duration of a GEMM config in the committed rocprofv3 trace of the headline
+    workload (written by bench/rocprof_summary.py), or None when the trace does not cover it."""
+    path = os.path.join(ROOT, "profiles", "gemm_prefill_p512_kernel_trace.json")
+    try:
+        prof = json.load(open(path))
+    except (OSError, ValueError):
+        return None
+    tag = cfg_tag(cfg_name)
+    for k in prof.get("kernels", []):
+        if tag and k["kernel"].endswith(tag):
+            return {"mean_us": k["mean_us"], "median_us": k["median_us"], "dispatches": k["dispatches"],
+                    "source": prof["source"]}
+    return None
 
 
 def measured_traffic(cfg_name, shapes):
@@ -176,19 +240,76 @@ def measured_traffic(cfg_name, shapes):
     key = {(2304, 768): "QKV 512x2304x768", (3072, 768): "fc 512x3072x768", (768, 768): "attn-proj 512x768x768",
            (768, 3072): "mlp-proj 512x768x3072"}
     want = [prof["per_shape"].get(key.get((x["N"], x["K"]), ""), {}) for x in shapes]
-    import re
-    m = re.fullmatch(r"dl_bn(\d+)_bm(\d+)_w(\d+)x(\d+)_s(\d+)(?:_k(\d+))?(?:_u(\d+))?", cfg_name)
-    if m:
-        g = m.groups()
-        tag = "k_gemm_dl<{}, {}, {}, {}, {}, false, {}, {}, 0>".format(*g[:5], g[5] or 1, g[6] or 1)
-    else:
-        m = re.fullmatch(r"bn(\d+)_bm(\d+)_bk(\d+)_w(\d+)x(\d+)_d(\d+)", cfg_name)
-        if not m:
-            return {}
-        tag = "k_gemm_mfma<{}, {}, {}, {}, {}, false, {}, false>".format(*m.groups())
-    if not want or any(not w or w.get("kernel") != tag for w in want):
+    tag = cfg_tag(cfg_name)
+    if not tag or not want or any(not w or w.get("kernel") != tag for w in want):
         return {}
     return {"traffic": round(sum(w["bytes"] for w in want) / len(want)), "traffic_source": prof["source"]}
+
+
+def launch_floor_us(B, iters=2000):
+    """An empty kernel (1 work-group) launched back to back on the launch stream: the per-launch floor
+    every GEMM, GEMV and graph node of this line pays."""
+    ms = C.c_float()
+    if B.H.gpt2_bench_empty(iters, C.byref(ms)):
+        B.pkg.check("gpt2_bench_empty")
+    return round(ms.value * 1e3, 3)
+
+
+def sustained_clock(B, ops, seconds=1.5):
+    """The shader clock under the headline workload: the same step run back to back for `seconds`
+    (untimed) while a second thread samples `amd-smi metric --clock` (one reading per XCD per sample);
+    median / min / max over every XCD reading.  The timed steps themselves last milliseconds, shorter
+    than one amd-smi call, so the clock is read under the same load right after them."""
+    import threading
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            c = amd_smi_clocks()
+            if not c:
+                return
+            samples.extend(v for k, v in c.items() if k.endswith(".clk.value") and isinstance(v, (int, float)))
+
+    t = threading.Thread(target=sampler, daemon=True)
+    t0 = time.perf_counter()
+    t.start()
+    n = 0
+    while time.perf_counter() - t0 < seconds:
+        B.run_ops(ops, 0, 20)
+        n += 1
+    stop.set()
+    t.join(timeout=30)
+    if not samples:
+        return {"sclk_mhz": None, "method": "amd-smi unavailable"}
+    return {"sclk_mhz_median": float(np.median(samples)), "sclk_mhz_min_max": [min(samples), max(samples)],
+            "readings": len(samples), "load_s": round(time.perf_counter() - t0, 2),
+            "method": "amd-smi metric --clock (every XCD's gfx clock) sampled in a thread while the headline step "
+                      f"ran back to back ({n * 20} steps, untimed) right after the timed region"}
+
+
+def amd_smi_clocks():
+    """The GPU clocks as `amd-smi metric --clock` reports them right after the headline's timed region
+    (the reference records the clock with every number, BENCH_PROTOCOL.md:64-72): the gfx entries of
+    its JSON, flattened; None where amd-smi is absent or refuses."""
+    import subprocess
+    try:
+        out = subprocess.run(["amd-smi", "metric", "--clock", "--json"], capture_output=True, text=True, timeout=20)
+        data = json.loads(out.stdout)
+    except (OSError, ValueError, subprocess.SubprocessError):
+        return None
+    flat = {}
+
+    def walk(x, path):
+        if isinstance(x, dict):
+            for k, v in x.items():
+                walk(v, f"{path}.{k}" if path else str(k))
+        elif isinstance(x, list):
+            for i, v in enumerate(x):
+                walk(v, f"{path}[{i}]")
+        elif "gfx" in path.lower() and len(flat) < 48:
+            flat[path] = x
+    walk(data, "")
+    return flat or None
 
 
 # ------------------------------------------------------------------------------ INT8 / fp16 GEMVs
@@ -234,6 +355,23 @@ def bench_gemv(B, quick=False):
                      "cold_us": round(ms_cold * 1e3, 3), "cold_GBs": round(algo / (ms_cold * 1e-3) / 1e9, 1),
                      "warm_us": round(ms_warm * 1e3, 3), "warm_GBs": round(algo / (ms_warm * 1e-3) / 1e9, 1)}
         big.free()
+        # the same shape with fp16 weights (gpt2_gemv_fp16): twice the weight bytes
+        algo16 = 2 * N * K + 2 * K + 2 * N + 2 * N
+        R16 = copies_for(2 * N * K)
+        big = B.empty(R16 * N * K * 2)
+        for r in range(R16):
+            L.gpt2_d2d(big.at(r * N * K * 2), w16.ptr, N * K * 2)
+        L.gpt2_sync()
+        ms16c, _ = B.run_ops([B.op(2, y.ptr, x.ptr, big.at(r * N * K * 2), None, b.ptr, 1, N, K) for r in range(R16)],
+                             1, n_cold)
+        ms16c /= R16
+        ms16w, _ = B.run_ops([B.op(2, y.ptr, x.ptr, w16.ptr, None, b.ptr, 1, N, K)], 5 if quick else 50, n_warm)
+        big.free()
+        res[name]["fp16"] = {"bytes": algo16, "copies": R16, "cold_us": round(ms16c * 1e3, 3),
+                             "cold_GBs": round(algo16 / (ms16c * 1e-3) / 1e9, 1), "warm_us": round(ms16w * 1e3, 3),
+                             "warm_GBs": round(algo16 / (ms16w * 1e-3) / 1e9, 1)}
+        res[name]["int8_speedup_cold"] = round(ms16c / ms_cold, 3)
+        res[name]["int8_speedup_warm"] = round(ms16w / ms_warm, 3)
         log(f"gemv {name}: {res[name]}")
     # the 48 INT8 GEMVs of one decode step, distinct weights per layer, back to back
     chain_bytes = 0
@@ -248,6 +386,8 @@ def bench_gemv(B, quick=False):
     ms_chain, _ = B.run_ops(chain, 2 if quick else 20, n_chain)
     res["trunk_chain_48"] = {"bytes": chain_bytes, "us": round(ms_chain * 1e3, 2),
                              "GBs": round(chain_bytes / (ms_chain * 1e-3) / 1e9, 1)}
+    if not quick:
+        res["trunk_chain_48"]["fp16_vs_int8"] = chain_fp16_vs_int8(B, chain, chain_bytes, x768, x3072, y, rng)
     # the same kernel on the INT8 tied head (38.6 MB, no bias): large enough that the launch floor
     # no longer hides the streaming rate
     N, K = VOCAB, 768
@@ -288,6 +428,36 @@ def bench_gemv(B, quick=False):
                 "warm_GBs": round(algo / (ms_warm * 1e-3) / 1e9, 1)}
     big.free()
     return res, head_res
+
+
+def chain_fp16_vs_int8(B, chain8, bytes8, x768, x3072, y, rng, rounds=12, burst=20):
+    """The 48 trunk GEMVs of one decode step with fp16 weights against the same chain with INT8 weights
+    (the reference's [C] comparison, BENCHMARKS.md:932: 0.9764 against 0.6948 ms), in alternating rounds
+    (fp16 first on even rounds); one sample = the mean of `burst` chains; median and [min, max] per side
+    and the overlap verdict (bench/ab.py)."""
+    ab = importlib.import_module("ab")
+    chain16, bytes16 = [], 0
+    for layer in range(N_LAYER):
+        for name, N, K in TRUNK_GEMV:
+            x = x3072 if K == 3072 else x768
+            W = B.dev(f16(rng, (N, K), 0.02))
+            b = B.dev(f16(rng, N, 0.01))
+            chain16.append(B.op(2, y.ptr, x.ptr, W.ptr, None, b.ptr, 1, N, K))
+            bytes16 += 2 * N * K + 2 * K + 4 * N
+    s16, s8 = [], []
+    B.run_ops(chain16, 5, 5)
+    for r in range(rounds):
+        for side in ((0, 1) if r % 2 == 0 else (1, 0)):
+            ms, _ = B.run_ops(chain16 if side == 0 else chain8, 2, burst)
+            (s16 if side == 0 else s8).append(ms * 1e3)
+    a, b8 = ab.stats(s16), ab.stats(s8)
+    v = ab.verdict(a, b8)
+    return {"fp16_us": {k: round(v_, 2) for k, v_ in a.items()}, "int8_us": {k: round(v_, 2) for k, v_ in b8.items()},
+            "fp16_bytes": bytes16, "int8_bytes": bytes8, "bytes_ratio": round(bytes16 / bytes8, 3),
+            "fp16_GBs": round(bytes16 / (a["median"] * 1e-6) / 1e9, 1),
+            "int8_GBs": round(bytes8 / (b8["median"] * 1e-6) / 1e9, 1),
+            "int8_speedup": v["speedup_b_vs_a"], "verdict": v["verdict"],
+            "rounds": rounds, "sample": f"mean of {burst} chains back to back, 48 distinct weights per chain"}
 
 
 # ------------------------------------------------------------------------------ INT8 GEMM set, head GEMM
@@ -571,17 +741,19 @@ def bench_decode(B, steady_reps=64, greedy=True, cold_copies=4, cold_reps=48):
     return res
 
 
-def decode_cold(B, scr, first, logits, tokens, streamed, kv_bytes, warm_ms, copies, reps):
-    """The persistent step with its weights cold: `copies` uploads of the same model, each with its own
-    K/V cache (the P=512 prefill) and graph, stepped round robin at pos 512, so the 162 MB of weights
-    a step reads were last read copies-1 steps (>= 487 MB of other weights) earlier, past the 256 MB
-    MALL.  The warm figure is the same step repeated on one copy."""
+def decode_cold(B, scr, first, logits, tokens, streamed, kv_bytes, warm_ms, copies, reps, backend="int8"):
+    """The default (persistent) step with its weights cold: `copies` uploads of the same model, each
+    with its own K/V cache (the P=512 prefill) and graph, stepped round robin at pos 512, so the weights
+    a step reads (162 MB INT8 trunk + fp16 head, 247 MB all fp16) were last read copies-1 steps earlier,
+    past the 256 MB MALL.  backend "int8" quantizes the trunk, "gemv" keeps every weight fp16.  With
+    first / streamed / kv_bytes / warm_ms left 0 / None, the step's own prefill token and byte counts
+    are used and no cold/warm ratio is given."""
     pkg, L = B.pkg, B.L
     synth = importlib.import_module("bare_metal_gpt2_amd.synth")
     P = 512
     ids = synth.token_ids(P, seed=1234)
     d_ids = B.dev(ids)
-    be = pkg.backend("int8")
+    be = pkg.backend(backend)
     caps = pkg.GPT2CapsGPU()
     caps.logits = logits.ptr
     caps.logits_all = 0
@@ -590,7 +762,8 @@ def decode_cold(B, scr, first, logits, tokens, streamed, kv_bytes, warm_ms, copi
     try:
         for _ in range(copies):
             m = pkg.Model(seeded_body())
-            m.quantize()
+            if backend == "int8":
+                m.quantize()
             kv = pkg.KVCache(1024)
             models.append(m)
             kvs.append(kv)
@@ -603,6 +776,12 @@ def decode_cold(B, scr, first, logits, tokens, streamed, kv_bytes, warm_ms, copi
             graphs.append(g)
         L.gpt2_sync()
         pkg.check("cold setup")
+        if not first:
+            first = int(np.argmax(pkg.half_bits_to_f32(logits.numpy(np.uint16, (VOCAB,)))))
+        if streamed is None:
+            streamed = models[0].q.streamed_bytes if backend == "int8" else FP16_STEP_WEIGHT_BYTES
+        if not kv_bytes:
+            kv_bytes = L.gpt2_kv_step_bytes(C.byref(kvs[0].kv), P + 1)
         samples = []
         for i in range(reps + copies):
             g = graphs[i % copies]
@@ -616,10 +795,13 @@ def decode_cold(B, scr, first, logits, tokens, streamed, kv_bytes, warm_ms, copi
                 pkg.check("cold decode")
         pkg.check("cold decode")
         med = float(np.median(samples))
-        return {"copies": copies, "rotated_weight_MB": round(copies * streamed / 1e6, 1),
-                "ms_step_at_512": round(med, 4), "tok_s_at_512": round(1000.0 / med, 1),
-                "step_GBs_at_512": round((streamed + kv_bytes) / (med * 1e-3) / 1e9, 1),
-                "cold_over_warm": round(med / warm_ms, 3)}
+        res = {"backend": backend, "copies": copies, "rotated_weight_MB": round(copies * streamed / 1e6, 1),
+               "ms_step_at_512": round(med, 4), "ms_step_min_max": [round(min(samples), 4), round(max(samples), 4)],
+               "tok_s_at_512": round(1000.0 / med, 1), "weight_bytes": int(streamed),
+               "step_GBs_at_512": round((streamed + kv_bytes) / (med * 1e-3) / 1e9, 1)}
+        if warm_ms:
+            res["cold_over_warm"] = round(med / warm_ms, 3)
+        return res
     finally:
         for g in graphs:
             L.gpt2_decode_graph_destroy(g)
@@ -627,6 +809,96 @@ def decode_cold(B, scr, first, logits, tokens, streamed, kv_bytes, warm_ms, copi
             kv.free()
         for m in models:
             m.free()
+
+
+FP16_STEP_WEIGHT_BYTES = 2 * 12 * (2304 * 768 + 768 * 768 + 3072 * 768 + 768 * 3072) + 2 * VOCAB * 768
+
+
+def bench_decode_compare(B, rounds=24, ctxs=(128, 512, 1023), cold_copies=4, cold_reps=32):
+    """fp16 against INT8 trunk weights in the decode step (the reference's central decode comparison,
+    BENCHMARKS.md:914-917): GPT-2-124M with fp16 trunk GEMVs (gemv backend) and with INT8 trunk GEMVs
+    (int8 backend), both with the fp16 head and the default (persistent) graph step; one P=1023 prefill
+    each, then single steps re-pinned at ctx 128, 512 and 1023 in alternating rounds (fp16 first on
+    even rounds).  Per (side, ctx): median and [min, max] of the single-step times; the INT8 speedup
+    and the overlap verdict.  Then both at ctx 512 with their weights cold (decode_cold)."""
+    pkg, L = B.pkg, B.L
+    ab = importlib.import_module("ab")
+    synth = importlib.import_module("bare_metal_gpt2_amd.synth")
+    P = 1023
+    ids = synth.token_ids(P, seed=1234)
+    d_ids = B.dev(ids)
+    sides, out = {}, {}
+    ms = C.c_float()
+    try:
+        for name, backend in (("fp16", "gemv"), ("int8", "int8")):
+            model = pkg.Model(seeded_body())
+            if backend == "int8":
+                model.quantize()
+            kv, scr = pkg.KVCache(1024), pkg.Scratch(1024)
+            logits, tokens = B.empty(VOCAB * 2), B.empty(1024 * 4)
+            caps = pkg.GPT2CapsGPU()
+            caps.logits, caps.logits_all = logits.ptr, 0
+            be = pkg.backend(backend)
+            sides[name] = {"model": model, "kv": kv, "scr": scr, "g": None}
+            L.gpt2_prefill_fill_cache(be, C.byref(model.gpu), C.byref(kv.kv), d_ids.ptr, P, C.byref(scr.s), C.byref(caps))
+            L.gpt2_sync()
+            pkg.check("prefill")
+            first = int(np.argmax(pkg.half_bits_to_f32(logits.numpy(np.uint16, (VOCAB,)))))
+            g = L.gpt2_decode_graph_create_mode(be, C.byref(model.gpu), C.byref(kv.kv), C.byref(scr.s), logits.ptr,
+                                                tokens.ptr, pkg.DECODE_AUTO)
+            if not g:
+                pkg.check("graph create")
+                raise RuntimeError("graph create failed")
+            sides[name].update(g=g, first=first, mode=L.gpt2_decode_graph_mode(g),
+                               weight_bytes=model.q.streamed_bytes if backend == "int8" else FP16_STEP_WEIGHT_BYTES)
+        samples = {(n, c): [] for n in sides for c in ctxs}
+        for r in range(rounds + 2):
+            for c in ctxs:
+                for n in (("fp16", "int8") if r % 2 == 0 else ("int8", "fp16")):
+                    sd = sides[n]
+                    L.gpt2_decode_graph_set(sd["g"], sd["first"], c)
+                    L.gpt2_decode_graph_time(sd["g"], 1, C.byref(ms))
+                    if r >= 2:
+                        samples[(n, c)].append(ms.value * 1e3)
+        tok, pos = C.c_int(), C.c_int()
+        for n, sd in sides.items():
+            if L.gpt2_decode_graph_sync(sd["g"], C.byref(tok), C.byref(pos)):
+                pkg.check(f"decode {n}")
+                raise RuntimeError("decode step failed")
+        for c in ctxs:
+            a, b = ab.stats(samples[("fp16", c)]), ab.stats(samples[("int8", c)])
+            v = ab.verdict(a, b)
+            kvb = L.gpt2_kv_step_bytes(C.byref(sides["int8"]["kv"].kv), c + 1)
+            row = {}
+            for n, st in (("fp16", a), ("int8", b)):
+                wb = sides[n]["weight_bytes"]
+                row[n] = {"us_median": round(st["median"], 2), "us_min_max": [round(st["min"], 2), round(st["max"], 2)],
+                          "tok_s": round(1e6 / st["median"], 1), "weight_bytes": wb,
+                          "step_GBs": round((wb + kvb) / (st["median"] * 1e-6) / 1e9, 1)}
+            row.update(int8_speedup=v["speedup_b_vs_a"], verdict=v["verdict"], kv_bytes=int(kvb))
+            out[f"ctx{c}"] = row
+        out["steps"] = {n: ("persistent (one kernel per token)" if sd["mode"] == pkg.DECODE_PERSISTENT
+                            else "multi-kernel graph") for n, sd in sides.items()}
+        out["rounds"] = rounds
+    finally:
+        for sd in sides.values():
+            if sd["g"]:
+                L.gpt2_decode_graph_destroy(sd["g"])
+            sd["kv"].free()
+            sd["scr"].free()
+            sd["model"].free()
+    if cold_copies:
+        scr = pkg.Scratch(1024)
+        logits, tokens = B.empty(VOCAB * 2), B.empty(1024 * 4)
+        try:
+            cold = {}
+            for n, backend in (("fp16", "gemv"), ("int8", "int8")):
+                cold[n] = decode_cold(B, scr, 0, logits, tokens, None, 0, None, cold_copies, cold_reps, backend=backend)
+            cold["int8_speedup"] = round(cold["fp16"]["ms_step_at_512"] / cold["int8"]["ms_step_at_512"], 3)
+            out["cold_ctx512"] = cold
+        finally:
+            scr.free()
+    return out
 
 
 # ------------------------------------------------------------------------------ persistent prefill trace
@@ -872,6 +1144,9 @@ def main():
     ap.add_argument("--prefill-trace", type=int, default=0, metavar="T",
                     help="only the persistent prefill at T tokens (INT8 and fp16) beside the launch sequence, "
                          "with its per-task trace, printed as one JSON line")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="only the headline GEMM set (no peaks, extras or CPU legs): the driver of the "
+                         "committed rocprofv3 trace that the roofline's kernel time is read from")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="also run one plain copy of BYTES (calibrates FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -912,9 +1187,10 @@ def main():
     if args.decode_only:
         print(json.dumps({"decode": bench_decode(B, steady_reps=32, greedy=False)}), flush=True)
         return
-    flops_step, ms_step, shapes, roofline, ms_graph = bench_gemm_set(B, args.steps, args.warmup)
+    flops_step, ms_step, shapes, roofline, ms_graph, step_stats, clock = bench_gemm_set(B, args.steps, args.warmup)
     value = flops_step / (ms_step * 1e-3) / 1e12
-    log(f"prefill GEMM set: {ms_step * 1e3:.1f} us/step -> {value:.1f} TFLOP/s; per shape {shapes}")
+    log(f"prefill GEMM set: {ms_step * 1e3:.1f} us/step -> {value:.1f} TFLOP/s; steps {step_stats}; clock {clock}")
+    log(f"per shape {shapes}")
     out = {"metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
@@ -923,10 +1199,14 @@ def main():
                                   "fp16 out (BASELINE config 2, per layer)",
                       "M": M_PREFILL, "layers": N_LAYER, "gflop_per_step": round(flops_step / 1e9, 4),
                       "device": name.value.decode()},
+           "step_stats": step_stats, "clock": clock, "launch_floor_us": launch_floor_us(B),
            "roofline": roofline, "gemm_shapes": shapes,
            "gemm_set_graph_replay": {"us_per_step": round(ms_graph * 1e3, 2),
                                      "tflops": round(flops_step / (ms_graph * 1e-3) / 1e12, 2)}}
     B.keep.clear()
+    if args.headline_only:
+        print(json.dumps(out), flush=True)
+        return
     peaks = measured_peaks(B, cus.value)
     out["measured_peaks"] = peaks
     roofline["peak_measured"] = peaks["mfma_fp16_tflops"]
@@ -953,6 +1233,9 @@ def main():
             out["decode"] = bench_decode(B)
             B.keep.clear()
             log(f"decode: {out['decode']}")
+            out["decode_fp16_vs_int8"] = bench_decode_compare(B)
+            B.keep.clear()
+            log(f"decode fp16 vs int8: {out['decode_fp16_vs_int8']}")
     out["bandwidth_guard"] = guard_legs(out, peaks["hbm_read_GBs"])
     if out["bandwidth_guard"]["suspicious"]:
         log(f"SUSPICIOUS (above the measured read stream): {out['bandwidth_guard']['suspicious']}")

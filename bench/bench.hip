@@ -8,13 +8,18 @@
 
 extern "C" {
 
-// Tuning hook of libgpt2amd.so (csrc/gemm.hip): one GEMM on a fixed tile config.
-void gpt2_tune_gemm_run(int cfg, gpt2_half *C, const gpt2_half *A, const void *W, const float *Ws,
-                        const gpt2_half *bias, int M, int N, int K);
-int gpt2_tune_gemm_fused(gpt2_half *C, const gpt2_half *A, const void *W, const float *Ws, const gpt2_half *bias,
-                         int M, int N, int K, int epi, const gpt2_half *resid);
-int gpt2_tune_gemm_ln(int cfg, gpt2_half *C, const gpt2_half *X, const gpt2_half *g, const gpt2_half *b, const void *W,
-                      const float *Ws, const gpt2_half *bias, int M, int N, int K, int epi);
+// Tuning hooks of libgpt2amd.so (csrc/gemm.hip): one GEMM on a fixed tile config, the fused-epilogue
+// GEMM, the LayerNorm-panel GEMM.  Weak, so this harness also loads against an older build of the
+// library that lacks them (bench/ab_build.sh); the ops that need a missing hook record an error.
+__attribute__((weak)) void gpt2_tune_gemm_run(int cfg, gpt2_half *C, const gpt2_half *A, const void *W,
+                                              const float *Ws, const gpt2_half *bias, int M, int N, int K);
+__attribute__((weak)) int gpt2_tune_gemm_fused(gpt2_half *C, const gpt2_half *A, const void *W, const float *Ws,
+                                               const gpt2_half *bias, int M, int N, int K, int epi,
+                                               const gpt2_half *resid);
+__attribute__((weak)) int gpt2_tune_gemm_ln(int cfg, gpt2_half *C, const gpt2_half *X, const gpt2_half *g,
+                                            const gpt2_half *b, const void *W, const float *Ws, const gpt2_half *bias,
+                                            int M, int N, int K, int epi);
+static int missing_hook = 0;
 
 // One timed operation: kind 0 = fp16 GEMM (gpt2_matmul_tiled), 1 = INT8 GEMM (gpt2_matmul_int8),
 // 2 = fp16 GEMV (gpt2_gemv_fp16), 3 = INT8 GEMV (gpt2_gemv_int8), 4 = causal prefill attention
@@ -43,14 +48,21 @@ static void run_op(const GPT2BenchOp &o) {
         case 4: gpt2_attention_flash(o.C, o.A, o.M, GPT2_N_EMBD, GPT2_N_HEAD, GPT2_HEAD_DIM); break;
         case 3: gpt2_gemv_int8(o.C, o.A, (const int8_t *)o.W, o.Ws, o.bias, o.N, o.K); break;
         case 5: gpt2_layernorm(o.C, o.A, (const gpt2_half *)o.W, o.bias, o.M, o.K); break;
-        case 6: gpt2_tune_gemm_fused(o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K, g2::EPI_RESID, o.C); break;
+        case 6:
+            if (gpt2_tune_gemm_fused) gpt2_tune_gemm_fused(o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K, g2::EPI_RESID, o.C);
+            else missing_hook = 1;
+            break;
         case 7: gpt2_add(o.C, o.A, (size_t)o.M * o.N); break;
-        case 8: gpt2_tune_gemm_fused(o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K, g2::EPI_GELU, nullptr); break;
+        case 8:
+            if (gpt2_tune_gemm_fused) gpt2_tune_gemm_fused(o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K, g2::EPI_GELU, nullptr);
+            else missing_hook = 1;
+            break;
         case 9: gpt2_gelu(o.C, (size_t)o.M * o.N); break;
         default:
-            if (o.kind >= 64)   // LayerNorm-panel GEMM on LN config kind - 64; the bias doubles as gamma and beta
+            if (o.kind >= 64 && gpt2_tune_gemm_ln)   // LayerNorm-panel GEMM on LN config kind - 64; the bias doubles as gamma and beta
                 gpt2_tune_gemm_ln(o.kind - 64, o.C, o.A, o.bias, o.bias, o.W, o.Ws, o.bias, o.M, o.N, o.K, 0);
-            else gpt2_tune_gemm_run(o.kind - 16, o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K);
+            else if (o.kind < 64 && gpt2_tune_gemm_run) gpt2_tune_gemm_run(o.kind - 16, o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K);
+            else missing_hook = 1;
             break;
     }
 }
@@ -88,6 +100,32 @@ int gpt2_bench_ops(const GPT2BenchOp *ops, int n, int warmup, int iters, float *
     }
     hipEventDestroy(a);
     hipEventDestroy(b);
+    return gpt2_last_error();
+}
+
+// Per-step timing: `warmup` untimed rounds of ops[0..n), then `iters` rounds, each between its own
+// pair of events (iters + 1 events recorded on the launch stream, consecutive rounds sharing one), so
+// the caller gets every round's time for a median and [min, max], not only their mean.  *ms_total is
+// first event to last.
+int gpt2_bench_ops_steps(const GPT2BenchOp *ops, int n, int warmup, int iters, float *ms_steps, float *ms_total) {
+    if (!ops || n <= 0 || iters <= 0 || !ms_steps) return 1;
+    hipStream_t s = (hipStream_t)gpt2_get_stream();
+    std::vector<hipEvent_t> ev(iters + 1, nullptr);
+    for (auto &e : ev)
+        if (hipEventCreate(&e) != hipSuccess) return 1;
+    for (int w = 0; w < warmup; ++w)
+        for (int i = 0; i < n; ++i) run_op(ops[i]);
+    hipStreamSynchronize(s);
+    hipEventRecord(ev[0], s);
+    for (int it = 0; it < iters; ++it) {
+        for (int i = 0; i < n; ++i) run_op(ops[i]);
+        hipEventRecord(ev[it + 1], s);
+    }
+    hipEventSynchronize(ev[iters]);
+    for (int it = 0; it < iters; ++it) hipEventElapsedTime(&ms_steps[it], ev[it], ev[it + 1]);
+    if (ms_total) hipEventElapsedTime(ms_total, ev[0], ev[iters]);
+    for (auto &e : ev) hipEventDestroy(e);
+    if (missing_hook) { missing_hook = 0; return 2; }
     return gpt2_last_error();
 }
 

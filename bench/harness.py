@@ -36,6 +36,7 @@ SIGNATURES = {
     "gpt2_bench_read": (_i, [_vp, _sz, _i, _fp]),
     "gpt2_bench_mfma": (_i, [_i, _i, _fp]),
     "gpt2_bench_copy": (_i, [_vp, _vp, _sz, _fp]),
+    "gpt2_bench_ops_steps": (_i, [C.POINTER(GPT2BenchOp), _i, _i, _i, _fp, _fp]),
 }
 
 _lib = None

@@ -178,8 +178,10 @@ int gpt2_quant_attach_if_needed(const GPT2Backend *be, GPT2WeightsGPU *gpu, GPT2
  * (tools/quantize.py:58-73: per output row, s = absmax/127 or 1 for a zero row,
  * q = clamp(rint(w/s), -127, 127)) and attaches the result to gpu->q, with no file.  keep[49] (may
  * be NULL) marks tensors left fp16, in the order wte, 12 x {qkv, attn_proj, fc, proj}; NULL keeps
- * only the head fp16 (the reference's default build).  No reference counterpart: it replaces the
- * offline quantize.py + file round trip.  Returns 0 on success. */
+ * only the head fp16 (the file the engine loads by default, weights/gpt2_124m_int8_kt.bin, is built
+ * that way); all-zero keep quantizes the head too (quantize.py's own default, --fp16-keep none).  No
+ * reference counterpart: it replaces the offline quantize.py + file round trip.  Returns 0 on
+ * success. */
 int gpt2_quant_build(GPT2WeightsGPU *gpu, GPT2QWeightsGPU *q, const int *keep);
 /* Device quantizer of one fp16 [N,K] tensor (the kernel gpt2_quant_build runs per tensor). */
 void gpt2_quantize_rows(int8_t *q, float *s, const gpt2_half *w, int N, int K);

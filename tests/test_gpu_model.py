@@ -627,3 +627,150 @@ def test_config5_decode_512_steps_vs_oracle(pkg, L, synth, model, int8_ref_body)
     assert kl.max() < 0.02, (int(np.argmax(kl)), float(kl.max()))
     # the prefill's last row against the oracle's row P-1
     assert rel_err(oracle.f16_to_f32(first_row)[None], ref[P - 1:P]) <= 1e-2
+
+
+# ------------------------------------------------------------------ every tensor INT8, the head included
+ALL_INT8 = [0] * 49     # tools/quantize.py:92 default --fp16-keep none: wte is quantized too
+
+
+@pytest.fixture(scope="module")
+def deq_head(synth, body):
+    """fl32(q*s) of the fp16 view of wte: the tied head as the INT8 build streams it
+    (tools/dequant_check.py:61-65); the embedding lookup keeps reading the fp16 wte."""
+    o, shape = synth.offsets()["wte"]
+    q, s, _ = oracle.quantize_fp16_view(body[o:o + int(np.prod(shape))].reshape(shape))
+    return oracle.dequantize(q, s).astype(np.float64)
+
+
+def oracle_int8_head_logits(int8_ref_body, deq_head, seq):
+    """Oracle logits of the all-INT8 model over seq: the oracle forward on the body with every trunk
+    matrix dequantized gives the final LayerNorm of every row; the head is that LayerNorm times the
+    dequantized wte (no bias, cuda/forward_cuda.cu:111-115), summed in float64."""
+    fin = oracle.forward(int8_ref_body, np.asarray(seq, np.int32), logits_all=False)["final_ln"]
+    return fin.astype(np.float64) @ deq_head.T
+
+
+def test_int8_head_persistent_step_vs_eager(pkg, L, synth, model):
+    """The persistent step's INT8-head branch (the head rows dequantized in registers) against the
+    eager step with the same all-INT8 weights, teacher-forced at positions 0, 1, 63, 511, 1022 and
+    1023 of a 1023-token prefill: rel_err <= 1e-2 and KL < 2e-3 per position, and the step's token is
+    the first argmax of its own logits."""
+    model.quantize(keep=ALL_INT8)
+    try:
+        assert model.q.wte.q, "head not quantized"
+        ids = synth.token_ids(1023, seed=31)
+        kv, scr, logits = decode_setup(pkg, L, model, ids, "int8")
+        be = pkg.backend("int8")
+        tokens = pkg.Dev(1024 * 4)
+        g = L.gpt2_decode_graph_create_mode(be, C.byref(model.gpu), C.byref(kv.kv), C.byref(scr.s), logits.ptr,
+                                            tokens.ptr, pkg.DECODE_PERSISTENT)
+        assert g, pkg.check("graph create")
+        try:
+            assert L.gpt2_decode_graph_mode(g) == pkg.DECODE_PERSISTENT
+            tok, pos = C.c_int(), C.c_int()
+            for p in (0, 1, 63, 511, 1022, 1023):
+                tok_in = int(ids[p]) if p < len(ids) else 17
+                kv.kv.len = len(ids)
+                L.gpt2_decode_step_cuda(be, C.byref(model.gpu), C.byref(kv.kv), tok_in, p, C.byref(scr.s),
+                                        logits.ptr, None)
+                pkg.check("eager step")
+                ref16 = logits.numpy(np.uint16, (V,)).copy()
+                assert L.gpt2_decode_graph_set(g, tok_in, p) == 0
+                assert L.gpt2_decode_graph_run(g, 1) == 0
+                assert L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)) == 0, pkg.check("persistent step")
+                assert pos.value == p + 1
+                lg = logits.numpy(np.uint16, (V,))
+                got, ref = oracle.f16_to_f32(lg)[None], oracle.f16_to_f32(ref16)[None]
+                assert rel_err(got, ref) <= 1e-2, (p, rel_err(got, ref))
+                assert kl_rows(ref, got).max() < 2e-3, p
+                assert tok.value == first_argmax(lg), p
+        finally:
+            L.gpt2_decode_graph_destroy(g)
+        scr.free()
+        kv.free()
+    finally:
+        L.gpt2_quant_free(C.byref(model.q))
+        model.q = None
+        model.gpu.q = None
+
+
+def test_int8_head_multi_kernel_graph_matches_eager(pkg, L, synth, model):
+    """The multi-kernel graph step with the head quantized uses the eager step's kernels in the same
+    order: 12 replays match 12 eager steps bit for bit (tokens and logits)."""
+    model.quantize(keep=ALL_INT8)
+    try:
+        ids = synth.token_ids(40, seed=32)
+        P, n = len(ids), 12
+        kv, scr, logits = decode_setup(pkg, L, model, ids, "int8")
+        first = first_argmax(logits.numpy(np.uint16, (V,)))
+        eager_toks, eager_rows = eager_greedy(pkg, L, model, kv, scr, logits, "int8", first, P, n)
+        kv.kv.len = P
+        tokens = pkg.Dev(1024 * 4)
+        g = L.gpt2_decode_graph_create_mode(pkg.backend("int8"), C.byref(model.gpu), C.byref(kv.kv),
+                                            C.byref(scr.s), logits.ptr, tokens.ptr, pkg.DECODE_MULTI)
+        assert g, pkg.check("graph create")
+        try:
+            assert L.gpt2_decode_graph_mode(g) == pkg.DECODE_MULTI
+            assert L.gpt2_decode_graph_set(g, first, P) == 0
+            tok, pos = C.c_int(), C.c_int()
+            for i in range(n):
+                assert L.gpt2_decode_graph_run(g, 1) == 0
+                assert L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)) == 0, pkg.check("graph step")
+                assert tok.value == eager_toks[i], i
+                assert np.array_equal(logits.numpy(np.uint16, (V,)), eager_rows[i]), i
+        finally:
+            L.gpt2_decode_graph_destroy(g)
+        scr.free()
+        kv.free()
+    finally:
+        L.gpt2_quant_free(C.byref(model.q))
+        model.q = None
+        model.gpu.q = None
+
+
+def test_int8_head_prefill_and_decode_vs_oracle(pkg, L, synth, model, int8_ref_body, deq_head):
+    """All 49 tensors INT8 (the reference quantizer's default): a P=64 prefill with logits for every
+    row, then 16 free-running greedy replays of the persistent step, against the oracle on the body
+    with every tensor dequantized, the head included.  Gates: rel_err <= 1e-2 per row and per step,
+    KL < 0.02; each step's token is the first argmax of its own logits."""
+    P, n = 64, 16
+    ids = synth.token_ids(P, seed=640)
+    model.quantize(keep=ALL_INT8)
+    try:
+        got_pre = gpu_forward(pkg, L, model, ids, "int8", logits_all=True)["logits"]
+        kv, scr, logits = decode_setup(pkg, L, model, ids, "int8")
+        first = first_argmax(logits.numpy(np.uint16, (V,)))
+        tokens = pkg.Dev(1024 * 4)
+        g = L.gpt2_decode_graph_create_mode(pkg.backend("int8"), C.byref(model.gpu), C.byref(kv.kv),
+                                            C.byref(scr.s), logits.ptr, tokens.ptr, pkg.DECODE_AUTO)
+        assert g, pkg.check("graph create")
+        rows, toks = [], []
+        try:
+            assert L.gpt2_decode_graph_mode(g) == pkg.DECODE_PERSISTENT
+            assert L.gpt2_decode_graph_set(g, first, P) == 0
+            tok, pos = C.c_int(), C.c_int()
+            for i in range(n):
+                assert L.gpt2_decode_graph_run(g, 1) == 0
+                assert L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)) == 0, pkg.check(f"step {i}")
+                lg = logits.numpy(np.uint16, (V,))
+                rows.append(lg)
+                assert tok.value == first_argmax(lg), i
+                toks.append(tok.value)
+        finally:
+            L.gpt2_decode_graph_destroy(g)
+        scr.free()
+        kv.free()
+    finally:
+        L.gpt2_quant_free(C.byref(model.q))
+        model.q = None
+        model.gpu.q = None
+    seq = np.concatenate([ids, [first], toks[:-1]]).astype(np.int32)
+    ref = oracle_int8_head_logits(int8_ref_body, deq_head, seq)
+    assert rel_err(got_pre, ref[:P]) <= 1e-2
+    assert kl_rows(ref[:P], got_pre).max() < 0.02
+    assert first == int(np.argmax(got_pre[-1]))
+    got = oracle.f16_to_f32(np.stack(rows))
+    refr = ref[P:P + n]
+    per_rel = [rel_err(got[i], refr[i]) for i in range(n)]
+    assert max(per_rel) <= 1e-2, per_rel
+    assert kl_rows(refr, got).max() < 0.02

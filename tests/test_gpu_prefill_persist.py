@@ -129,9 +129,10 @@ def test_persistent_prefill_vs_oracle(pkg, L, synth, model, backend, T):
 
 def test_persistent_timeout_is_reported(pkg, L, synth, model):
     """Error path forced from the host: with a zero-round poll limit the first task that finds a
-    counter short gives up, every work-group leaves, gpt2_prefill_status reports it (and clears it),
-    and the next launch with the default limit is whole again (the last work-group cleared the
-    counters and the ticket)."""
+    counter short gives up and every work-group leaves; the next synchronizing call (gpt2_sync)
+    reports it through its return code and gpt2_last_error (and clears the sticky word), and the next
+    launch with the default limit is whole again (the last work-group cleared the counters and the
+    ticket).  gpt2_prefill_status reports a second timed-out launch when it is read first."""
     T = 96
     ids = synth.token_ids(T, seed=3)
     d_ids = pkg.Dev.from_numpy(np.asarray(ids, np.int32))
@@ -143,10 +144,17 @@ def test_persistent_timeout_is_reported(pkg, L, synth, model):
     L.gpt2_tune_prefill_spin(0)
     L.gpt2_tune_prefill_persistent(1)
     try:
+        L.gpt2_last_error()
         L.gpt2_prefill_fill_cache(pkg.backend("flash"), C.byref(model.gpu), C.byref(kv.kv), d_ids.ptr, T,
                                   C.byref(scr.s), C.byref(caps))
-        L.gpt2_sync()
-        assert L.gpt2_prefill_status() != 0
+        assert L.gpt2_sync() != 0
+        assert L.gpt2_last_error() != 0
+        assert L.gpt2_prefill_status() == 0      # the sync took (and cleared) the sticky word
+        L.gpt2_prefill_fill_cache(pkg.backend("flash"), C.byref(model.gpu), C.byref(kv.kv), d_ids.ptr, T,
+                                  C.byref(scr.s), C.byref(caps))
+        assert L.gpt2_prefill_status() != 0      # read directly, before any gpt2_sync
+        assert L.gpt2_sync() == 0
+        L.gpt2_last_error()
     finally:
         L.gpt2_tune_prefill_spin(-1)
         L.gpt2_tune_prefill_persistent(-1)

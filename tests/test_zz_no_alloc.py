@@ -5,7 +5,10 @@ so it matches gpt2_forward_cuda with that kernel switched off (the default) bit 
 rows, the final LayerNorm, every layer's residual stream and the K/V cache it fills -- and
 gpt2_forward_cuda with the persistent kernel switched on within the fp16 gates.  Two calls in a row, the second with fewer tokens
 (the array keeps the first call's contents), for the fp16 and the INT8 backend; and a call past the
-static limit is refused with an error and writes nothing."""
+static limit is refused with an error and writes nothing.  The property itself: across a call, the
+library's allocation count (every device allocation goes through gpt2_dmalloc) and the device's free
+memory (hipMemGetInfo) do not change; and one call captured into a HIP graph, replayed three times
+with eager work between the replays, matches the eager call bit for bit on every replay."""
 import ctypes as C
 
 import numpy as np
@@ -96,3 +99,88 @@ def test_forward_noalloc_rejects_past_limit(pkg, L, synth, model):
     L.gpt2_sync()
     assert L.gpt2_last_error() != 0
     assert np.array_equal(logits.numpy(np.uint16, (V,)), sentinel)
+
+
+def test_forward_noalloc_allocates_nothing(pkg, L, synth, model):
+    """The no-allocation property, measured: after one warm-up call (the first call on a device
+    resolves the static array's address and loads the kernels), a second call changes neither the
+    library's count of gpt2_dmalloc calls nor the device's free memory."""
+    T = 64
+    ids = synth.token_ids(T, seed=77)
+    d_ids = pkg.Dev.from_numpy(np.asarray(ids, np.int32))
+    logits = pkg.Dev(T * V * 2)
+    caps = pkg.GPT2CapsGPU()
+    caps.logits, caps.logits_all = logits.ptr, 1
+    be = pkg.backend("flash")
+    L.gpt2_forward_noalloc(be, C.byref(model.gpu), d_ids.ptr, T, C.byref(caps))
+    L.gpt2_sync()
+    pkg.check("warm-up call")
+    n0, f0 = L.gpt2_test_dmalloc_calls(), L.gpt2_test_mem_free()
+    L.gpt2_forward_noalloc(be, C.byref(model.gpu), d_ids.ptr, T, C.byref(caps))
+    L.gpt2_sync()
+    pkg.check("second call")
+    n1, f1 = L.gpt2_test_dmalloc_calls(), L.gpt2_test_mem_free()
+    assert f0 > 0
+    assert n1 == n0, f"gpt2_dmalloc called {n1 - n0} times"
+    assert f1 == f0, f"free device memory changed by {f0 - f1} bytes"
+
+
+def hip_runtime():
+    h = C.CDLL("libamdhip64.so")
+    for name in ("hipStreamCreate", "hipStreamBeginCapture", "hipStreamEndCapture", "hipGraphInstantiate",
+                 "hipGraphLaunch", "hipStreamSynchronize", "hipGraphExecDestroy", "hipGraphDestroy",
+                 "hipStreamDestroy"):
+        getattr(h, name).restype = C.c_int
+    return h
+
+
+def test_forward_noalloc_under_graph_capture(pkg, L, synth, model):
+    """gpt2_forward_noalloc captured into a HIP graph on a stream of its own (gpt2_set_stream resolves
+    the static array's address before the capture begins), the graph replayed three times; between
+    the replays the eager call runs again on other ids, so each replay starts from the array holding
+    another call's contents.  Every replay matches the eager call on the same ids bit for bit, and the
+    whole sequence (capture, instantiation aside) makes no gpt2_dmalloc call."""
+    hip = hip_runtime()
+    T = 48
+    ids, other = synth.token_ids(T, seed=91), synth.token_ids(T, seed=92)
+    d_ids, d_other = pkg.Dev.from_numpy(np.asarray(ids, np.int32)), pkg.Dev.from_numpy(np.asarray(other, np.int32))
+    logits, fin = pkg.Dev(T * V * 2), pkg.Dev(T * E * 2)
+    caps = pkg.GPT2CapsGPU()
+    caps.logits, caps.logits_all, caps.final_ln = logits.ptr, 1, fin.ptr
+    be = pkg.backend("flash")
+
+    def eager(d):
+        L.gpt2_forward_noalloc(be, C.byref(model.gpu), d.ptr, T, C.byref(caps))
+        L.gpt2_sync()
+        pkg.check("eager noalloc")
+        return logits.numpy(np.uint16, (T * V,)).copy(), fin.numpy(np.uint16, (T * E,)).copy()
+
+    ref = eager(d_ids)
+    stream, graph, exe = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    assert hip.hipStreamCreate(C.byref(stream)) == 0
+    try:
+        L.gpt2_set_stream(stream)
+        n0 = L.gpt2_test_dmalloc_calls()
+        assert hip.hipStreamBeginCapture(stream, 1) == 0          # hipStreamCaptureModeThreadLocal
+        L.gpt2_forward_noalloc(be, C.byref(model.gpu), d_ids.ptr, T, C.byref(caps))
+        assert hip.hipStreamEndCapture(stream, C.byref(graph)) == 0
+        pkg.check("capture")
+        assert L.gpt2_test_dmalloc_calls() == n0
+        assert hip.hipGraphInstantiate(C.byref(exe), graph, None, None, 0) == 0
+        for r in range(3):
+            eager(d_other)                                          # the array now holds another call
+            L.gpt2_memset(logits.ptr, 0, T * V * 2)
+            assert hip.hipGraphLaunch(exe, stream) == 0
+            assert hip.hipStreamSynchronize(stream) == 0
+            pkg.check("replay")
+            got = (logits.numpy(np.uint16, (T * V,)), fin.numpy(np.uint16, (T * E,)))
+            for name, a, b in zip(("logits", "final_ln"), got, ref):
+                assert np.array_equal(a, b), f"replay {r}: {name} differs in {np.count_nonzero(a != b)} elements"
+        assert L.gpt2_test_dmalloc_calls() == n0
+    finally:
+        L.gpt2_set_stream(None)
+        if exe:
+            hip.hipGraphExecDestroy(exe)
+        if graph:
+            hip.hipGraphDestroy(graph)
+        hip.hipStreamDestroy(stream)
