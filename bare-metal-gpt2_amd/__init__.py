@@ -156,6 +156,8 @@ SIGNATURES = {
     "gpt2_tune_decode_spin": (None, [_i]),
     "gpt2_tune_decode_trace": (None, [_vp]),
     "gpt2_tune_prefill_fused": (None, [_i]),
+    "gpt2_tune_prefill_lnfold": (None, [_i]),
+    "gpt2_tune_prefill_lnfold_sites": (_i, []),
     "gpt2_decode_graph_set": (_i, [_vp, _i, _i]),
     "gpt2_decode_graph_run": (_i, [_vp, _i]),
     "gpt2_decode_graph_sync": (_i, [_vp, C.POINTER(C.c_int), C.POINTER(C.c_int)]),

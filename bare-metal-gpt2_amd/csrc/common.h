@@ -165,8 +165,38 @@ __device__ __forceinline__ uint16_t gelu_f16(float v) {
     return f2h(y);
 }
 
-// Elementwise op fused into a matmul's epilogue: none, gelu_new, or a residual add.
-enum { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2 };
+// Elementwise op fused into a matmul's epilogue: none, gelu_new, or a residual add; and the forms
+// of the prefill's LayerNorm fold (LnFold below): the residual add that also emits x * gamma and the
+// row statistics, and the matmul over x * gamma that applies the LayerNorm in its epilogue (then
+// gelu_new for the fc matmul).
+enum { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2, EPI_RESID_LN = 3, EPI_LNF = 4, EPI_LNF_GELU = 5 };
+
+// LayerNorm folded into the matmul that consumes it.  For a row x (768 wide) with mean mu and
+// rstd = 1 / sqrt(var + eps),
+//   LN(x) . W_n = rstd (sum_k x_k g_k W_nk - mu sum_k g_k W_nk) + sum_k b_k W_nk
+// so the consumer multiplies xg = x * gamma (fp16) by W and finishes each output with
+//   rstd_m (P_mn - mu_m G_n) + H_n,   G_n = sum_k gamma_k W_nk,  H_n = sum_k beta_k W_nk
+// (fp32, per consumer matrix; INT8: W_nk = s_n q_nk).  mu and var come from per-row partial sums
+// of the fp16 x (sum, sum of squares), one partial per 16-column slice of the row, each written by
+// the one wave that produced those columns: 48 slots per row, summed in a fixed order by the
+// consumer, so the result does not depend on which work-group finishes first.  The partials are
+// stored slot-major with a slot stride of lnfold_stride(M) rows: an odd number of 128-byte lines
+// (from M = 16 up), so the slots of a row block spread over the L2 channels instead of lining up
+// on one (a stride of M = 512 rows is 4 KB).
+constexpr int LNF_SLOTS = GPT2_N_EMBD / 16;
+inline int lnfold_stride(int M) {
+    if (M < 16) return M;
+    const int r = (M + 15) & ~15;
+    return (r / 16) % 2 ? r : r + 16;
+}
+struct LnFold {
+    const uint16_t *gamma;   // RESID_LN: gamma of the LayerNorm the x feeds (fp16, 768)
+    uint16_t *xg;            // RESID_LN: x * gamma, fp16, row-major like C
+    float2 *stats_out;       // RESID_LN: [LNF_SLOTS][stride] (sum x, sum x^2) of 16 columns each
+    const float2 *stats_in;  // LNF: the producer's stats of the A rows
+    const float2 *gh;        // LNF: (G_n, H_n) per output column
+    int stride;              // rows per slot in the partials: lnfold_stride(M)
+};
 
 // A GEMM output after scale and bias, as the unfused sequence would leave it: rounded to fp16, then
 // gelu (rounded again) or the residual r added (rounded again) -- the rounding points of a separate
@@ -174,8 +204,8 @@ enum { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2 };
 template <int EPI>
 __device__ __forceinline__ uint16_t epi_out(float v, uint16_t r) {
     uint16_t o = f2h(v);
-    if constexpr (EPI == EPI_GELU) o = gelu_f16(h2f(o));
-    else if constexpr (EPI == EPI_RESID) o = f2h(h2f(r) + h2f(o));
+    if constexpr (EPI == EPI_GELU || EPI == EPI_LNF_GELU) o = gelu_f16(h2f(o));
+    else if constexpr (EPI == EPI_RESID || EPI == EPI_RESID_LN) o = f2h(h2f(r) + h2f(o));
     return o;
 }
 

@@ -29,6 +29,13 @@ void argmax_advance(const uint16_t *logits, int V, int *state, int *tokens, int 
 void attn_decode_append(uint16_t *att, const uint16_t *qkv, uint16_t *K, uint16_t *V, int maxT, StepArg st);
 bool gemv_fused(uint16_t *C, const uint16_t *x, const void *W, const float *Ws, const uint16_t *bias, int N, int K,
                 bool qw, const uint16_t *ln_g, const uint16_t *ln_b, int epi, const uint16_t *resid);
+int gemm_ln_forced();
+bool gemm_lnfold(int epi, uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const uint16_t *bias, int M,
+                 int N, int K, bool qw, const uint16_t *resid, const LnFold &lf);
+void embed_lnf(uint16_t *x, uint16_t *xg, float2 *stats, const uint16_t *wte, const uint16_t *wpe, const int *ids,
+               int T, const uint16_t *gamma);
+void ln_fold_consts(float2 *gh, const void *W, const float *Ws, const uint16_t *gamma, const uint16_t *beta, int N,
+                    int K, bool qw);
 }  // namespace g2
 
 using namespace g2;
@@ -185,8 +192,11 @@ extern "C" void gpt2_upload_fp16(const GPT2Weights *cpu, GPT2WeightsGPU *gpu) {
     gpu->q = nullptr;
 }
 
+static void fold_consts_drop(const void *wdata, const void *qdata);
+
 extern "C" void gpt2_free_gpu(GPT2WeightsGPU *g) {
     if (g && g->data) {
+        fold_consts_drop(g->data, nullptr);
         gpt2_dfree(g->data);
         g->data = nullptr;
     }
@@ -263,10 +273,106 @@ static void ln_matmul_site(const GPT2Backend *be, bool fused, bool ln_fuse, gpt2
     else matmul_site(be, fused, C, lnbuf, Wh, Wq, bias, M, N, K, epi, nullptr);
 }
 
-// persistent: the trunk may run as the persistent kernel (it allocates its arena on first use, so
-// the no-allocation entry point runs the launch sequence instead).
+// ---------------------------------------------------------------------------- LayerNorm fold
+// The fused prefill folds LN1 and LN2 into the GEMMs that consume them.  With mu, rstd the row's
+// mean and 1/sqrt(var + eps) and x*gamma the row scaled by the LayerNorm's gamma,
+//     LayerNorm(x) . W_n = rstd (x*gamma . W_n - mu G_n) + H_n,  G_n = sum_k gamma_k W_nk,
+//                                                                H_n = sum_k beta_k W_nk,
+// so the GEMM producing x (the embedding, attn-proj, mlp-proj) also writes x*gamma of the next
+// LayerNorm and 48 partial row sums (sum x, sum x^2 over each 16-column slice, fp32), and the
+// consumer (QKV, fc) multiplies x*gamma by W and finishes the LayerNorm in its epilogue -- 24
+// LayerNorm launches, and their read and write of the activations, fewer per forward.  The result is
+// not bit-identical to LayerNorm-then-GEMM: the fp16 rounding moves from the normalized row to
+// x*gamma (same relative size), and the variance comes from the sums (E[x^2] - mu^2, fp32).
+//
+// G and H depend on the weights only: computed once per weights (and INT8 codes) on first use,
+// cached per device, dropped by gpt2_free_gpu / gpt2_quant_free.  Weights changed in place need
+// gpt2_tune_prefill_lnfold(0) or a fresh upload.
+//
+// By default the fold runs where it measured faster (interleaved A/B of the whole prefill, fold on
+// against off, MI355X): T <= 128 for both weight formats (7-13% faster), INT8 up to T = 256 (4-5%).
+// Past that the fold's per-tile costs (the partials' loads and the producer's extra stores in every
+// work-group) outgrow the two LayerNorm launches it removes per layer: even at T = 384-512, 0.97-0.92
+// at T = 768-1024.
+static int g_lnfold = -1;       // gpt2_tune_prefill_lnfold: -1 default (by T), 0 off, 1 on at every T > 1
+static int g_lnfold_sites = 0;  // sites that ran folded in the last forward (test hook)
+
+extern "C" void gpt2_tune_prefill_lnfold(int on) { g_lnfold = on < 0 ? -1 : (on != 0); }
+extern "C" int gpt2_tune_prefill_lnfold_sites(void) { return g_lnfold_sites; }
+
+static bool lnfold_wanted(int T, bool int8) {
+    if (g_lnfold >= 0) return g_lnfold == 1;
+    return T <= (int8 ? 256 : 128);
+}
+
+constexpr int FOLD_ROW = GPT2_QKV_DIM + GPT2_FFN_DIM;   // (G, H) pairs per layer: QKV's, then fc's
+
+struct FoldConsts {
+    const void *wdata;   // fp16 body
+    const void *qdata;   // INT8 codes in use, or null
+    int dev;
+    float2 *gh;          // [layer][FOLD_ROW]
+};
+static std::mutex g_fold_mu;
+static std::vector<FoldConsts> g_fold;
+
+static void fold_consts_drop(const void *wdata, const void *qdata) {
+    std::lock_guard<std::mutex> lock(g_fold_mu);
+    for (size_t i = 0; i < g_fold.size();) {
+        if ((wdata && g_fold[i].wdata == wdata) || (qdata && g_fold[i].qdata == qdata)) {
+            int cur = 0;
+            (void)hipGetDevice(&cur);
+            if (cur != g_fold[i].dev) (void)hipSetDevice(g_fold[i].dev);
+            gpt2_dfree(g_fold[i].gh);
+            if (cur != g_fold[i].dev) (void)hipSetDevice(cur);
+            g_fold[i] = g_fold.back();
+            g_fold.pop_back();
+        } else {
+            ++i;
+        }
+    }
+}
+
+// The (G, H) table of these weights on the current device, computed on the stream when first asked
+// for; null when it cannot be had now (no allocation under stream capture, allocation failure).
+static const float2 *fold_consts(const GPT2Backend *be, const GPT2WeightsGPU *w) {
+    const GPT2QWeightsGPU *qw = be->matmul_q ? w->q : nullptr;
+    const void *qdata = qw ? (const void *)qw->qdata : nullptr;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(g_fold_mu);
+    for (const FoldConsts &f : g_fold)
+        if (f.wdata == w->data && f.qdata == qdata && f.dev == dev) return f.gh;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream(), &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    // an allocation failure is not the caller's (the unfolded sequence runs instead); an error the
+    // caller has not read yet stays recorded
+    const int pending = gpt2_last_error();
+    float2 *gh = (float2 *)gpt2_dmalloc((size_t)GPT2_N_LAYER * FOLD_ROW * sizeof(float2));
+    (void)gpt2_last_error();
+    if (pending) set_error(pending, "an earlier call (recorded before the LayerNorm fold's set-up)");
+    if (!gh) return nullptr;
+    for (int L = 0; L < GPT2_N_LAYER; ++L) {
+        const GPT2LayerGPU *ly = &w->layers[L];
+        const GPT2QLayerGPU *qy = qw ? &qw->layers[L] : nullptr;
+        const bool qq = qy && qy->qkv_w.q, qf = qy && qy->fc_w.q;
+        ln_fold_consts(gh + (size_t)L * FOLD_ROW, qq ? (const void *)qy->qkv_w.q : ly->qkv_w, qq ? qy->qkv_w.s : nullptr,
+                       ly->ln1_g, ly->ln1_b, GPT2_QKV_DIM, GPT2_N_EMBD, qq);
+        ln_fold_consts(gh + (size_t)L * FOLD_ROW + GPT2_QKV_DIM, qf ? (const void *)qy->fc_w.q : ly->fc_w,
+                       qf ? qy->fc_w.s : nullptr, ly->ln2_g, ly->ln2_b, GPT2_FFN_DIM, GPT2_N_EMBD, qf);
+    }
+    g_fold.push_back(FoldConsts{w->data, qdata, dev, gh});
+    return gh;
+}
+
+// may_alloc: the trunk may run as the persistent kernel, and the LayerNorm fold may build its
+// constants (both allocate on first use, so the no-allocation entry point runs the unfolded launch
+// sequence instead).
 static void forward_impl(const GPT2Backend *be, const GPT2WeightsGPU *w, const int *d_ids, int T, GPT2ScratchGPU *s,
-                         GPT2CapsGPU *caps, bool persistent);
+                         GPT2CapsGPU *caps, bool may_alloc);
 
 extern "C" void gpt2_forward_cuda(const GPT2Backend *be, const GPT2WeightsGPU *w, const int *d_ids, int T,
                                   GPT2ScratchGPU *s, GPT2CapsGPU *caps) {
@@ -274,7 +380,7 @@ extern "C" void gpt2_forward_cuda(const GPT2Backend *be, const GPT2WeightsGPU *w
 }
 
 static void forward_impl(const GPT2Backend *be, const GPT2WeightsGPU *w, const int *d_ids, int T, GPT2ScratchGPU *s,
-                         GPT2CapsGPU *caps, bool persistent) {
+                         GPT2CapsGPU *caps, bool may_alloc) {
     if (!be || !w || !w->data || !s || !d_ids || T <= 0 || T > s->maxT || T > GPT2_N_CTX) {
         arg_fail("gpt2_forward_cuda: bad arguments (T must be in [1, min(maxT, 1024)])");
         return;
@@ -288,7 +394,8 @@ static void forward_impl(const GPT2Backend *be, const GPT2WeightsGPU *w, const i
     // With the persistent prefill switched on (off by default: slower than the launch sequence),
     // the 12-layer trunk runs as one kernel (prefill.hip); the final LayerNorm, the head and the
     // captures follow as launches.
-    if (fused && persistent) {
+    g_lnfold_sites = 0;
+    if (fused && may_alloc) {
         const uint16_t *x0 = nullptr, *xl[GPT2_N_LAYER];
         const uint16_t *xf = prefill_persist(be, w, d_ids, T, kv, &x0, xl);
         if (xf) {
@@ -308,25 +415,85 @@ static void forward_impl(const GPT2Backend *be, const GPT2WeightsGPU *w, const i
     // the attention launch fills the cache itself when it is this library's prefill attention
     const bool attn_kv = fused && be->attention == gpt2_attention_flash && kv && kv->data;
     const bool ln_fuse = fused && be->layernorm == gpt2_layernorm;
-    be->embed(s->x, w->wte, w->wpe, d_ids, T, E);
+    // The LayerNorm fold (above): this library's embedding and LayerNorm, T > 1 (the single-row GEMMs
+    // are GEMVs), no forced LayerNorm-panel config.  x*gamma lives in s->ln, the row partials in
+    // s->ao (48 x lnfold_stride(T) float2, at most T + 31 rows: within its T x 1536 bytes from T = 11
+    // up, and T itself below 16); `have_stats` says whether the partials of the current x are there
+    // -- a site whose fold kernel is not available runs unfolded and clears it, and the next
+    // LayerNorm then runs as a launch.
+    const float2 *gh = nullptr;
+    if (fused && may_alloc && T > 1 && lnfold_wanted(T, be->matmul_q && qw) && be->embed == gpt2_embed &&
+        be->layernorm == gpt2_layernorm && gemm_ln_forced() < 0)
+        gh = fold_consts(be, w);
+    float2 *stats = reinterpret_cast<float2 *>(s->ao);
+    bool have_stats = false;
+    if (gh) {
+        embed_lnf(s->x, s->ln, stats, w->wte, w->wpe, d_ids, T, w->layers[0].ln1_g);
+        have_stats = true;
+    } else {
+        be->embed(s->x, w->wte, w->wpe, d_ids, T, E);
+    }
     if (caps && caps->embed) capcpy(caps->embed, s->x, (size_t)T * E);
     for (int L = 0; L < GPT2_N_LAYER; ++L) {
         const GPT2LayerGPU *ly = &w->layers[L];
         const GPT2QLayerGPU *qy = qw ? &qw->layers[L] : nullptr;
-        ln_matmul_site(be, fused, ln_fuse, s->qkv, s->x, ly->ln1_g, ly->ln1_b, s->ln, ly->qkv_w,
-                       qy ? &qy->qkv_w : nullptr, ly->qkv_b, T, Q, E, EPI_NONE);
+        const bool qq = be->matmul_q && qy && qy->qkv_w.q, qf = be->matmul_q && qy && qy->fc_w.q;
+        const bool qa = be->matmul_q && qy && qy->attn_proj_w.q, qp = be->matmul_q && qy && qy->proj_w.q;
+        LnFold lf{};
+        lf.stats_in = stats;
+        lf.stride = lnfold_stride(T);
+        lf.gh = gh ? gh + (size_t)L * FOLD_ROW : nullptr;
+        if (have_stats && gemm_lnfold(EPI_LNF, s->qkv, s->ln, qq ? (const void *)qy->qkv_w.q : ly->qkv_w,
+                                      qq ? qy->qkv_w.s : nullptr, ly->qkv_b, T, Q, E, qq, nullptr, lf))
+            ++g_lnfold_sites;
+        else
+            ln_matmul_site(be, fused, ln_fuse, s->qkv, s->x, ly->ln1_g, ly->ln1_b, s->ln, ly->qkv_w,
+                           qy ? &qy->qkv_w : nullptr, ly->qkv_b, T, Q, E, EPI_NONE);
+        have_stats = false;
         if (attn_kv && L < kv->nLayer) {
             attention_prefill(s->att, s->qkv, T, gpt2_kv_K(kv, L), gpt2_kv_V(kv, L), kv->maxT);
         } else {
             if (kv) gpt2_kv_scatter_prefill(kv, L, s->qkv, T);
             be->attention(s->att, s->qkv, T, E, H, D);
         }
-        matmul_site(be, fused, s->x, s->att, ly->attn_proj_w, qy ? &qy->attn_proj_w : nullptr, ly->attn_proj_b, T, E, E,
-                    EPI_RESID, s->ao);
-        ln_matmul_site(be, fused, ln_fuse, s->fc, s->x, ly->ln2_g, ly->ln2_b, s->ln, ly->fc_w,
-                       qy ? &qy->fc_w : nullptr, ly->fc_b, T, F, E, EPI_GELU);
-        matmul_site(be, fused, s->x, s->fc, ly->proj_w, qy ? &qy->proj_w : nullptr, ly->proj_b, T, E, F, EPI_RESID,
-                    s->ff);
+        lf = LnFold{};
+        lf.gamma = ly->ln2_g;
+        lf.xg = s->ln;
+        lf.stats_out = stats;
+        lf.stride = lnfold_stride(T);
+        if (gh && gemm_lnfold(EPI_RESID_LN, s->x, s->att, qa ? (const void *)qy->attn_proj_w.q : ly->attn_proj_w,
+                              qa ? qy->attn_proj_w.s : nullptr, ly->attn_proj_b, T, E, E, qa, s->x, lf)) {
+            ++g_lnfold_sites;
+            have_stats = true;
+        } else {
+            matmul_site(be, fused, s->x, s->att, ly->attn_proj_w, qy ? &qy->attn_proj_w : nullptr, ly->attn_proj_b, T,
+                        E, E, EPI_RESID, s->ao);
+        }
+        lf = LnFold{};
+        lf.stats_in = stats;
+        lf.stride = lnfold_stride(T);
+        lf.gh = gh ? gh + (size_t)L * FOLD_ROW + Q : nullptr;
+        if (have_stats && gemm_lnfold(EPI_LNF_GELU, s->fc, s->ln, qf ? (const void *)qy->fc_w.q : ly->fc_w,
+                                      qf ? qy->fc_w.s : nullptr, ly->fc_b, T, F, E, qf, nullptr, lf))
+            ++g_lnfold_sites;
+        else
+            ln_matmul_site(be, fused, ln_fuse, s->fc, s->x, ly->ln2_g, ly->ln2_b, s->ln, ly->fc_w,
+                           qy ? &qy->fc_w : nullptr, ly->fc_b, T, F, E, EPI_GELU);
+        have_stats = false;
+        lf = LnFold{};
+        lf.gamma = L + 1 < GPT2_N_LAYER ? w->layers[L + 1].ln1_g : nullptr;
+        lf.xg = s->ln;
+        lf.stats_out = stats;
+        lf.stride = lnfold_stride(T);
+        if (gh && lf.gamma &&
+            gemm_lnfold(EPI_RESID_LN, s->x, s->fc, qp ? (const void *)qy->proj_w.q : ly->proj_w,
+                        qp ? qy->proj_w.s : nullptr, ly->proj_b, T, E, F, qp, s->x, lf)) {
+            ++g_lnfold_sites;
+            have_stats = true;
+        } else {
+            matmul_site(be, fused, s->x, s->fc, ly->proj_w, qy ? &qy->proj_w : nullptr, ly->proj_b, T, E, F, EPI_RESID,
+                        s->ff);
+        }
         if (caps && caps->blocks) capcpy(caps->blocks + (size_t)L * T * E, s->x, (size_t)T * E);
     }
     be->layernorm(s->ln, s->x, w->lnf_g, w->lnf_b, T, E);
@@ -768,6 +935,7 @@ void q_attach(GPT2QWeightsGPU *q, const int *quantized) {
 
 extern "C" void gpt2_quant_free(GPT2QWeightsGPU *q) {
     if (!q) return;
+    if (q->qdata) fold_consts_drop(nullptr, q->qdata);
     gpt2_dfree(q->qdata);
     gpt2_dfree(q->sdata);
     q->qdata = nullptr;

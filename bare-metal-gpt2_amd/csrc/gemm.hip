@@ -283,7 +283,8 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
                                         const void *__restrict__ Wv, const float *__restrict__ Ws,
                                         const uint16_t *__restrict__ bias, int M, int N, int K, int tiles_m,
                                         int ntiles, int flags, const uint16_t *resid,
-                                        const uint16_t *__restrict__ ln_g, const uint16_t *__restrict__ ln_b) {
+                                        const uint16_t *__restrict__ ln_g, const uint16_t *__restrict__ ln_b,
+                                        const LnFold &lf) {
 #if defined(__HIP_DEVICE_COMPILE__)   // LDS address-space pointers exist only in the device pass
     // flags: bit 0 = C rows are 8-byte aligned (vector stores); bits 4-7 = gn, the XCD block grid
     // (see below; 0 = contiguous runs of tiles per XCD).
@@ -306,8 +307,19 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
     static_assert(S >= 2 && (S - 2) * LMAX < 64, "stages");
     static_assert(U >= 1 && S % U == 0 && S >= 2 * U, "k-tiles per barrier");
 
-    __shared__ __attribute__((aligned(1024))) char smem_all[KS * S * STAGE + PANEL];
+    // LayerNorm fold (LnFold): EPI_RESID_LN writes x*gamma of the next LayerNorm and each row's
+    // partial sums; EPI_LNF / EPI_LNF_GELU finish the LayerNorm of A = x*gamma in the epilogue.  The
+    // FG waves that share a block of rows (the WN column waves of every k group) split the 48 row
+    // partials FSL apiece and meet in a small LDS area after the panel (part of the one LDS object).
+    constexpr bool RLN = EPI == EPI_RESID_LN, LNF = EPI == EPI_LNF || EPI == EPI_LNF_GELU;
+    static_assert(!(RLN || LNF) || (!LNP && SK == 1), "the LayerNorm fold is a plain direct-to-LDS form");
+    constexpr int FG = WN * KS, FSL = LNF_SLOTS / FG;
+    static_assert(!LNF || (FSL * FG == LNF_SLOTS && FSL % 4 == 0), "row partials split evenly, 4 lane groups");
+    constexpr int FOLD_LDS = LNF ? FG * BM * 8 : 0;
+
+    __shared__ __attribute__((aligned(1024))) char smem_all[KS * S * STAGE + PANEL + FOLD_LDS];
     char *const panel = smem_all + KS * S * STAGE;   // LNP: 12 k-tile blocks of A, as a ring stage lays them out
+    float2 *const fold_red = reinterpret_cast<float2 *>(smem_all + KS * S * STAGE + PANEL);   // [FG][BM]
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -434,9 +446,18 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
     // k group that stores (4 scattered 2-byte loads per block, in every k group, cost 0.8-2.3 us per
     // launch in request traffic).  (The residual may alias C: this lane is the only one that writes
     // these elements, in the epilogue.)
+    // The LayerNorm fold's operands the same way: RESID_LN the next LayerNorm's gamma of the lane's
+    // columns; LNF each column's (G, H) and, per row, the lane's share of the producer's row partials
+    // (stored slot-major, [slot][row]: 16 lanes of a lane group read 16 consecutive rows of one slot;
+    // fold member fgi takes slots fgi * FSL + lgrp + 4 j), summed below before the k-loop.
     uint32_t bs_e[TN][4];            // fp16 bias bits, zero-extended
     float sc_e[TN][4];
     uint2 rs2[TN][TM];               // fp16 residual bits, 4 columns packed
+    uint32_t gm_e[RLN ? TN : 1][4];  // fp16 gamma bits
+    float2 gh_e[LNF ? TN : 1][4];
+    constexpr int QSLOT = LNF ? FSL / 4 : 1;
+    const int fgi = wave / WM + WN * kg;
+    float2 st_e[LNF ? TM : 1][QSLOT];
 #pragma unroll
     for (int a = 0; a < TN; ++a) {
         const int nb = n0 + wn0 + a * 16 + lgrp * 4;
@@ -446,14 +467,25 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
             sc_e[a][i] = 1.f;
             if constexpr (QW) sc_e[a][i] = Ws[n];
             bs_e[a][i] = *(bias ? bias + n : A);
+            if constexpr (RLN) gm_e[a][i] = lf.gamma[n];
+            if constexpr (LNF) gh_e[a][i] = lf.gh[n];
         }
 #pragma unroll
         for (int b = 0; b < TM; ++b) {
             rs2[a][b] = uint2{0u, 0u};
-            if constexpr (EPI == EPI_RESID)
+            if constexpr (EPI == EPI_RESID || RLN)
                 if (KS == 1 || kg == 0)
                     rs2[a][b] = *reinterpret_cast<const uint2 *>(
                         resid + (size_t)min(m0 + wm0 + b * 16 + lrow, M - 1) * N + min(nb, N - 4));
+        }
+    }
+    if constexpr (LNF) {
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+            const float2 *sr =
+                lf.stats_in + (size_t)(fgi * FSL + lgrp) * lf.stride + min(m0 + wm0 + b * 16 + lrow, M - 1);
+#pragma unroll
+            for (int j = 0; j < QSLOT; ++j) st_e[b][j] = sr[(size_t)4 * j * lf.stride];
         }
     }
     auto rs_at = [&](int a, int b, int i) -> uint16_t {
@@ -485,6 +517,26 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
     // Prologue: tiles 0 .. S-U-1 in flight (the config table requires nk >= S - U, nk % U == 0).
 #pragma unroll
     for (int s = 0; s < S - U; ++s) issue(s);
+    // LNF: this wave's FSL partials of each row (loaded before the tiles): each lane sums its
+    // slots, lanes lrow + 16 g exchange (a fixed pairing: the four lanes of the row end with the same
+    // bits), and lane group 0 leaves the sum in the fold area; the k-loop's barriers (it runs at least
+    // once) publish it to the epilogue.
+    if constexpr (LNF) {
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+            float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+            for (int j = 0; j < QSLOT; ++j) {
+                s1 += st_e[b][j].x;
+                s2 += st_e[b][j].y;
+            }
+            s1 += __shfl_xor(s1, 16);
+            s2 += __shfl_xor(s2, 16);
+            s1 += __shfl_xor(s1, 32);
+            s2 += __shfl_xor(s2, 32);
+            if (lgrp == 0) fold_red[fgi * BM + wm0 + b * 16 + lrow] = float2{s1, s2};
+        }
+    }
     if constexpr (LNP) {
         const int chunk = (lane & 15) >> 1;
 #pragma unroll
@@ -604,8 +656,29 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
                 acc[a][b] = sum;
             }
     }
+    // LNF: each row's mean and rstd from the FG member sums, added in member order (every wave of
+    // the row block gets the same bits).
+    float mu_e[LNF ? TM : 1], rsd_e[LNF ? TM : 1];
+    if constexpr (LNF) {
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+            float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+            for (int g = 0; g < FG; ++g) {
+                const float2 p = fold_red[g * BM + wm0 + b * 16 + lrow];
+                s1 += p.x;
+                s2 += p.y;
+            }
+            const float mean = s1 * (1.0f / GPT2_N_EMBD);
+            const float var = fmaxf(s2 * (1.0f / GPT2_N_EMBD) - mean * mean, 0.f);
+            mu_e[b] = mean;
+            rsd_e[b] = 1.0f / sqrtf(var + GPT2_LN_EPS);
+        }
+    }
     // Epilogue: lane holds D[n][m] for n = nb..nb+3, m = mrow.
     if (!vec_store) {
+        if constexpr (RLN || LNF) return;   // the host runs the fold only where C rows are 8-byte aligned
+        else {
         // Rows of C that are not 8-byte aligned (odd N: the tied head's 50257 columns): the tile
         // is staged in the now idle LDS ring and leaves row by row, a wave writing 64 consecutive
         // column pairs per store (dword-aligned in C; a lone first or last column as a 2-byte
@@ -643,6 +716,7 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
             if (lane == 1 && ((ncols - head) & 1)) dst[ncols - 1] = src[ncols - 1];
         }
         return;
+        }
     }
     if (kg != 0) return;
 #pragma unroll
@@ -651,14 +725,39 @@ __device__ __forceinline__ void gemm_dl(uint16_t *__restrict__ C, const uint16_t
 #pragma unroll
         for (int b = 0; b < TM; ++b) {
             const int m = m0 + wm0 + b * 16 + lrow;
-            if (m >= M) continue;
             uint16_t o[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float v = acc[a][b][i];
                 if constexpr (QW) v = v * sc_e[a][i];
+                // LNF: v is x*gamma . W_n; the row's LayerNorm finishes it (then the bias, gelu)
+                if constexpr (LNF) v = __builtin_fmaf(rsd_e[b], v - mu_e[b] * gh_e[a][i].x, gh_e[a][i].y);
                 o[i] = epi_out<EPI>(v + (bias ? h2f((uint16_t)bs_e[a][i]) : 0.f), rs_at(a, b, i));
             }
+            if constexpr (RLN) {
+                // x * gamma for the consumer, and the row's sums over these 16 columns: the lane's 4,
+                // then the four lane groups of the row (every lane joins the exchange; rows past M
+                // store nothing)
+                float s1 = 0.f, s2 = 0.f;
+                uint16_t g4[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float xv = h2f(o[i]);
+                    s1 += xv;
+                    s2 = __builtin_fmaf(xv, xv, s2);
+                    g4[i] = f2h(xv * h2f((uint16_t)gm_e[a][i]));
+                }
+                s1 += __shfl_xor(s1, 16);
+                s2 += __shfl_xor(s2, 16);
+                s1 += __shfl_xor(s1, 32);
+                s2 += __shfl_xor(s2, 32);
+                if (m < M) {
+                    *reinterpret_cast<uint2 *>(lf.xg + (size_t)m * N + nb) =
+                        uint2{(uint32_t)g4[0] | ((uint32_t)g4[1] << 16), (uint32_t)g4[2] | ((uint32_t)g4[3] << 16)};
+                    if (lgrp == 0) lf.stats_out[(size_t)((n0 + wn0 + a * 16) / 16) * lf.stride + m] = float2{s1, s2};
+                }
+            }
+            if (m >= M) continue;
             uint16_t *dst = C + (size_t)m * N + nb;
             if (vec_store && nb + 3 < N) {
                 const uint2 pk = {(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
@@ -680,7 +779,7 @@ __global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl(uint16_t *__restri
                                                          int tiles_m, int ntiles, int vec_store,
                                                          const uint16_t *resid) {
     gemm_dl<BN, BM, WN, WM, S, QW, KS, U, EPI, false>(C, A, Wv, Ws, bias, M, N, K, tiles_m, ntiles, vec_store, resid,
-                                                      nullptr, nullptr);
+                                                      nullptr, nullptr, LnFold{});
 }
 
 // k_gemm_dl with K split over SK work-groups per tile (grid = tiles x SK): for tiles large enough
@@ -691,7 +790,19 @@ __global__ __launch_bounds__(WN *WM * 64) void k_gemm_sk(uint16_t *__restrict__ 
                                                     const uint16_t *__restrict__ bias, int M, int N, int K,
                                                     int tiles_m, int ntiles, int vec_store, const uint16_t *resid) {
     gemm_dl<BN, BM, WN, WM, S, QW, 1, U, EPI, false, SK>(C, A, Wv, Ws, bias, M, N, K, tiles_m, ntiles, vec_store,
-                                                         resid, nullptr, nullptr);
+                                                         resid, nullptr, nullptr, LnFold{});
+}
+
+// k_gemm_dl with the prefill's LayerNorm fold (EPI_RESID_LN, EPI_LNF, EPI_LNF_GELU; LnFold).
+template <int BN, int BM, int WN, int WM, int S, bool QW, int KS, int U, int EPI>
+__global__ __launch_bounds__(WN *WM * KS * 64) void k_gemm_dl_lnf(uint16_t *__restrict__ C,
+                                                             const uint16_t *__restrict__ A,
+                                                             const void *__restrict__ Wv, const float *__restrict__ Ws,
+                                                             const uint16_t *__restrict__ bias, int M, int N, int K,
+                                                             int tiles_m, int ntiles, int vec_store,
+                                                             const uint16_t *resid, LnFold lf) {
+    gemm_dl<BN, BM, WN, WM, S, QW, KS, U, EPI, false>(C, A, Wv, Ws, bias, M, N, K, tiles_m, ntiles, vec_store, resid,
+                                                      nullptr, nullptr, lf);
 }
 
 // C = LayerNorm(X; ln_g, ln_b) . W^T (+ bias) (then gelu for EPI_GELU), K = 768: the prefill's
@@ -708,7 +819,7 @@ __global__ __launch_bounds__(WN *WM * 64) void k_gemm_dl_ln(uint16_t *__restrict
                                                        const uint16_t *__restrict__ ln_g,
                                                        const uint16_t *__restrict__ ln_b) {
     gemm_dl<BN, BM, WN, WM, S, QW, 1, U, EPI, true>(C, X, Wv, Ws, bias, M, N, K, tiles_m, ntiles, vec_store, nullptr,
-                                                    ln_g, ln_b);
+                                                    ln_g, ln_b, LnFold{});
 }
 
 // Any shape, any alignment: 16x16 outputs per work-group, k staged through LDS as fp32.
@@ -888,6 +999,52 @@ static const GemmLnCfg kLnCfgs[] = {
 };
 static const int kNumLnCfgs = (int)(sizeof(kLnCfgs) / sizeof(kLnCfgs[0]));
 
+// The LayerNorm fold's kernels, on the configs the pick table gives each role: the residual GEMMs
+// (attn-proj, mlp-proj: EPI_RESID_LN) and the GEMMs after a LayerNorm (QKV: EPI_LNF, fc:
+// EPI_LNF_GELU), fp16 and INT8 weights, every M bucket.  A call whose picked config has no entry
+// here (a forced config) runs the LayerNorm launch and the plain GEMM instead.
+typedef void (*GemmLnfFn)(uint16_t *, const uint16_t *, const void *, const float *, const uint16_t *, int, int, int,
+                          int, int, int, const uint16_t *, LnFold);
+struct GemmLnfEntry {
+    int cfg;
+    bool qw;
+    int epi;
+    GemmLnfFn fn;
+};
+#define G2_LNF(CFG, QW, EPI, BN, BM, WN, WM, S, KS, U) {CFG, QW, EPI, k_gemm_dl_lnf<BN, BM, WN, WM, S, QW, KS, U, EPI>}
+static const GemmLnfEntry kLnfKernels[] = {
+    // residual GEMMs: fp16 attn-proj 8, 25, 36 / mlp-proj 47, 23, 5; INT8 attn-proj 47, 31, 36 / mlp-proj 45, 36
+    G2_LNF(5, false, EPI_RESID_LN, 64, 64, 2, 4, 4, 1, 1),
+    G2_LNF(8, false, EPI_RESID_LN, 32, 32, 1, 2, 4, 1, 1),
+    G2_LNF(23, false, EPI_RESID_LN, 48, 32, 3, 2, 6, 2, 2),
+    G2_LNF(25, false, EPI_RESID_LN, 48, 32, 3, 2, 6, 1, 2),
+    G2_LNF(36, false, EPI_RESID_LN, 48, 64, 3, 2, 4, 2, 2),
+    G2_LNF(47, false, EPI_RESID_LN, 32, 32, 1, 2, 4, 4, 1),
+    G2_LNF(31, true, EPI_RESID_LN, 48, 32, 3, 2, 8, 1, 4),
+    G2_LNF(36, true, EPI_RESID_LN, 48, 64, 3, 2, 4, 2, 2),
+    G2_LNF(45, true, EPI_RESID_LN, 48, 32, 3, 1, 4, 4, 2),
+    G2_LNF(47, true, EPI_RESID_LN, 32, 32, 1, 2, 4, 4, 1),
+    // QKV: fp16 8, 29, 35, 0; INT8 47, 39, 36, 35
+    G2_LNF(0, false, EPI_LNF, 96, 64, 2, 4, 4, 1, 1),
+    G2_LNF(8, false, EPI_LNF, 32, 32, 1, 2, 4, 1, 1),
+    G2_LNF(29, false, EPI_LNF, 48, 64, 3, 4, 6, 1, 3),
+    G2_LNF(35, false, EPI_LNF, 48, 32, 3, 1, 4, 1, 2),
+    G2_LNF(35, true, EPI_LNF, 48, 32, 3, 1, 4, 1, 2),
+    G2_LNF(36, true, EPI_LNF, 48, 64, 3, 2, 4, 2, 2),
+    G2_LNF(39, true, EPI_LNF, 48, 32, 3, 1, 6, 2, 2),
+    G2_LNF(47, true, EPI_LNF, 32, 32, 1, 2, 4, 4, 1),
+    // fc: fp16 8, 40, 26, 6; INT8 47, 39, 36, 35, 1
+    G2_LNF(6, false, EPI_LNF_GELU, 128, 128, 2, 4, 4, 1, 1),
+    G2_LNF(8, false, EPI_LNF_GELU, 32, 32, 1, 2, 4, 1, 1),
+    G2_LNF(26, false, EPI_LNF_GELU, 48, 64, 3, 4, 4, 1, 2),
+    G2_LNF(40, false, EPI_LNF_GELU, 48, 32, 3, 1, 8, 1, 4),
+    G2_LNF(1, true, EPI_LNF_GELU, 128, 64, 4, 2, 3, 1, 1),
+    G2_LNF(35, true, EPI_LNF_GELU, 48, 32, 3, 1, 4, 1, 2),
+    G2_LNF(36, true, EPI_LNF_GELU, 48, 64, 3, 2, 4, 2, 2),
+    G2_LNF(39, true, EPI_LNF_GELU, 48, 32, 3, 1, 6, 2, 2),
+    G2_LNF(47, true, EPI_LNF_GELU, 32, 32, 1, 2, 4, 4, 1),
+};
+
 static int g_force_cfg = -2;  // -2: not read yet; -1: table
 
 static bool cfg_fits(int c, int K) { return K % kCfgs[c].kmul == 0 && K >= kCfgs[c].kmin; }
@@ -1055,6 +1212,7 @@ bool gemm_fused(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, 
 // before its first MFMA (24 to 48 work-groups per row block), each wave reducing 6 to 11 rows in
 // sequence, and the 48 KB panel halves the work-groups resident per CU.
 static int g_ln_cfg = -1;   // >= 0: the prefill's QKV and fc run that config; -1: off
+int gemm_ln_forced() { return g_ln_cfg; }
 
 // C = LayerNorm(X; ln_g, ln_b) . W^T (+ bias), then gelu for EPI_GELU, in one launch (K = 768).
 // cfg < 0 takes the forced config, if any.  Returns false (nothing launched) when no LayerNorm-panel kernel
@@ -1073,6 +1231,39 @@ bool gemm_ln(uint16_t *C, const uint16_t *X, const uint16_t *ln_g, const uint16_
                        Ws, bias, M, N, K, tiles_m, ntiles, vec, ln_g, ln_b);
     check_launch(qw ? "k_gemm_dl_ln<int8>" : "k_gemm_dl_ln<fp16>");
     return true;
+}
+
+// One matmul of the prefill's LayerNorm fold (LnFold): EPI_RESID_LN (C = resid + A.W^T + b into C,
+// plus x*gamma and the row partials; N = 768) or EPI_LNF / EPI_LNF_GELU (A = x*gamma, K = 768).
+// Returns false (nothing launched) when the picked config has no fold kernel, for M = 1, or where C
+// (and the residual) rows are not 8-byte aligned -- the caller then runs the unfolded sequence.
+bool gemm_lnfold(int epi, uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const uint16_t *bias, int M,
+                 int N, int K, bool qw, const uint16_t *resid, const LnFold &lf) {
+    if (M <= 1 || N <= 0 || K <= 0 || !mfma_ok(A, W, K, qw) || N % 4 || ((uintptr_t)C & 7u)) return false;
+    if (lf.stride < M) return false;
+    if (epi == EPI_RESID_LN) {
+        if (N != GPT2_N_EMBD || !resid || ((uintptr_t)resid & 7u) || ((uintptr_t)lf.xg & 7u) || !lf.gamma ||
+            !lf.stats_out)
+            return false;
+    } else if (epi == EPI_LNF || epi == EPI_LNF_GELU) {
+        if (K != GPT2_N_EMBD || !lf.stats_in || !lf.gh) return false;
+    } else {
+        return false;
+    }
+    const int c = pick_cfg(M, N, K, qw);
+    if (c < 0) return false;
+    for (const GemmLnfEntry &e : kLnfKernels) {
+        if (e.cfg != c || e.qw != qw || e.epi != epi) continue;
+        const GemmCfg &g = kCfgs[c];
+        if (!cfg_usable(c, M, N, K)) return false;
+        const int tiles_m = cdiv(M, g.bm), tiles_n = cdiv(N, g.bn);
+        const int ntiles = tiles_m * tiles_n;
+        hipLaunchKernelGGL(e.fn, dim3(ntiles), dim3(g.threads), 0, stream(), C, A, W, Ws, bias, M, N, K, tiles_m,
+                           ntiles, 1 | (xcd_blocks(g, tiles_m, tiles_n, K, qw) << 4), resid, lf);
+        check_launch("k_gemm_dl_lnf");
+        return true;
+    }
+    return false;
 }
 
 }  // namespace g2

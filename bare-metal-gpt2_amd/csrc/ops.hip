@@ -40,6 +40,85 @@ __global__ void k_embed_one(uint16_t *__restrict__ x, const uint16_t *__restrict
     x[e] = f2h(te + pe);
 }
 
+// The embedding for the prefill's LayerNorm fold (LnFold): one wave per row writes x = wte + wpe,
+// xg = x * gamma (gamma of the first layer's LN1) and the row's 48 partial sums (sum x, sum x^2 over
+// each 16-column slice) of the fp16 x, slot-major ([slot][stride], as the fold's GEMMs read them).  Lane l holds columns 256 i + 4 l + c (i < 3, c < 4), so
+// slice 16 i + l / 4 is the four lanes 4 (l / 4) .. +3, reduced with two fixed lane exchanges.
+__global__ __launch_bounds__(256) void k_embed_lnf(uint16_t *__restrict__ x, uint16_t *__restrict__ xg,
+                                                   float2 *__restrict__ stats, const uint16_t *__restrict__ wte,
+                                                   const uint16_t *__restrict__ wpe, const int *__restrict__ ids,
+                                                   const uint16_t *__restrict__ gamma, int T, int stride) {
+    constexpr int E = GPT2_N_EMBD;
+    const int lane = threadIdx.x & 63;
+    const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (row >= T) return;   // wave-uniform
+    const int id = ids[row];
+    const bool in_vocab = (unsigned)id < (unsigned)GPT2_VOCAB;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int c0 = 256 * i + 4 * lane;
+        uint16_t o[4], g[4];
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float te = in_vocab ? h2f(wte[(size_t)id * E + c0 + c]) : 0.f;
+            o[c] = f2h(te + h2f(wpe[(size_t)row * E + c0 + c]));
+            const float xv = h2f(o[c]);
+            s1 += xv;
+            s2 = __builtin_fmaf(xv, xv, s2);
+            g[c] = f2h(xv * h2f(gamma[c0 + c]));
+        }
+        *reinterpret_cast<uint2 *>(x + (size_t)row * E + c0) =
+            uint2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+        *reinterpret_cast<uint2 *>(xg + (size_t)row * E + c0) =
+            uint2{(uint32_t)g[0] | ((uint32_t)g[1] << 16), (uint32_t)g[2] | ((uint32_t)g[3] << 16)};
+        s1 += __shfl_xor(s1, 1);
+        s2 += __shfl_xor(s2, 1);
+        s1 += __shfl_xor(s1, 2);
+        s2 += __shfl_xor(s2, 2);
+        if ((lane & 3) == 0) stats[(size_t)(16 * i + lane / 4) * stride + row] = float2{s1, s2};
+    }
+}
+
+// The LayerNorm fold's per-column constants of one consumer matrix W [N, K] (fp16, or INT8 codes with
+// row scales): G_n = sum_k gamma_k W_nk, H_n = sum_k beta_k W_nk, fp32 (INT8: the code sums times
+// s_n, as the consumer scales its code sums).  One wave per row.
+template <bool QW>
+__global__ __launch_bounds__(256) void k_ln_fold_consts(float2 *__restrict__ gh, const void *__restrict__ Wv,
+                                                        const float *__restrict__ Ws, const uint16_t *__restrict__ gamma,
+                                                        const uint16_t *__restrict__ beta, int N, int K) {
+    const int lane = threadIdx.x & 63;
+    const int n = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (n >= N) return;
+    float g = 0.f, h = 0.f;
+    for (int k = lane; k < K; k += 64) {
+        const float w = QW ? (float)reinterpret_cast<const int8_t *>(Wv)[(size_t)n * K + k]
+                           : h2f(reinterpret_cast<const uint16_t *>(Wv)[(size_t)n * K + k]);
+        g = __builtin_fmaf(h2f(gamma[k]), w, g);
+        h = __builtin_fmaf(h2f(beta[k]), w, h);
+    }
+    g = wave_sum(g);
+    h = wave_sum(h);
+    const float s = QW ? Ws[n] : 1.f;
+    if (lane == 0) gh[n] = float2{g * s, h * s};
+}
+
+void embed_lnf(uint16_t *x, uint16_t *xg, float2 *stats, const uint16_t *wte, const uint16_t *wpe, const int *ids,
+               int T, const uint16_t *gamma) {
+    hipLaunchKernelGGL(k_embed_lnf, dim3(cdiv(T, 4)), dim3(256), 0, stream(), x, xg, stats, wte, wpe, ids, gamma, T,
+                       lnfold_stride(T));
+    check_launch("k_embed_lnf");
+}
+
+void ln_fold_consts(float2 *gh, const void *W, const float *Ws, const uint16_t *gamma, const uint16_t *beta, int N,
+                    int K, bool qw) {
+    if (qw)
+        hipLaunchKernelGGL(k_ln_fold_consts<true>, dim3(cdiv(N, 4)), dim3(256), 0, stream(), gh, W, Ws, gamma, beta, N, K);
+    else
+        hipLaunchKernelGGL(k_ln_fold_consts<false>, dim3(cdiv(N, 4)), dim3(256), 0, stream(), gh, W, Ws, gamma, beta, N, K);
+    check_launch("k_ln_fold_consts");
+}
+
 // ------------------------------------------------------------------ LayerNorm: one wave per row
 template <bool VEC768>
 __global__ __launch_bounds__(256) void k_layernorm(uint16_t *__restrict__ out, const uint16_t *__restrict__ x,

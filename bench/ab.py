@@ -22,7 +22,7 @@ SPEC: comma-separated key=value knobs; an empty SPEC ("") is the library's defau
   lib=DIR        a build of the library in DIR (libgpt2amd.so + libgpt2bench.so, see ab_build.sh);
                  a side with lib= runs in worker subprocesses, alternated with the other side's
   gemm_cfg=C     force GEMM tile config C for every call (gpt2_tune_gemm_force; -1 = the picks)
-  prefill_persistent=0|1, backend=int8|gemv|flash, pos=P, T=T, mode=persistent|multi,
+  prefill_persistent=0|1, lnfold=0|1 (the prefill's LayerNorm fold), backend=int8|gemv|flash, pos=P, T=T, mode=persistent|multi,
   dtype=int8|fp16, shape=qkv|attn_proj|fc|mlp_proj, big_alloc=GiB (allocate, touch and free that
   much device memory before the workload's own buffers, as bench.py's measured peaks leg does)
 
@@ -286,6 +286,8 @@ class PrefillWorkload:
         model, kv, scr, d_ids, caps = self.state(backend, T)
         if hasattr(L, "gpt2_tune_prefill_persistent"):
             L.gpt2_tune_prefill_persistent(int(knobs.get("prefill_persistent", -1)))
+        if hasattr(L, "gpt2_tune_prefill_lnfold"):
+            L.gpt2_tune_prefill_lnfold(int(knobs.get("lnfold", -1)))
         be = env.pkg.backend(backend)
         out = []
         for _ in range(5):
@@ -296,6 +298,8 @@ class PrefillWorkload:
             out.append((time.perf_counter() - t) * 1e6)
         if hasattr(L, "gpt2_tune_prefill_persistent"):
             L.gpt2_tune_prefill_persistent(-1)
+        if hasattr(L, "gpt2_tune_prefill_lnfold"):
+            L.gpt2_tune_prefill_lnfold(-1)
         env.pkg.check("prefill")
         return float(np.median(out[1:]))
 

@@ -121,16 +121,18 @@ def test_prefill_forward_backends_agree(pkg, L, synth, model):
                                           ("flash", 200, 1), ("int8", 512, 2)])
 def test_fused_prefill_bit_identical(pkg, L, synth, model, backend, T, ln):
     """The fused launch sequence of the prefill (gelu and the residual adds in GEMM epilogues, the K/V
-    cache fill inside the attention launch; the persistent trunk kernel switched off) equals the
-    unfused reference sequence bit for bit: every layer's residual stream, the final LayerNorm, all
-    logits rows and the whole K/V cache.  ln >= 0 also runs LN1 -> QKV and LN2 -> fc as
-    LayerNorm-panel GEMMs with that config (at T where the plain GEMMs have one k group)."""
+    cache fill inside the attention launch; the persistent trunk kernel and the LayerNorm fold
+    switched off) equals the unfused reference sequence bit for bit: every layer's residual stream,
+    the final LayerNorm, all logits rows and the whole K/V cache.  ln >= 0 also runs LN1 -> QKV and
+    LN2 -> fc as LayerNorm-panel GEMMs with that config (at T where the plain GEMMs have one k group).
+    The fold moves rounding points; test_gpu_lnfold holds it to the fp16 gates."""
     ids = synth.token_ids(T, seed=T + 7)
     d_ids = pkg.Dev.from_numpy(np.asarray(ids, np.int32))
     if backend == "int8":
         model.quantize()
     runs = []
     L.gpt2_tune_prefill_persistent(0)
+    L.gpt2_tune_prefill_lnfold(0)
     try:
         for fused in (1, 0):
             L.gpt2_tune_prefill_fused(fused)
@@ -155,6 +157,7 @@ def test_fused_prefill_bit_identical(pkg, L, synth, model, backend, T, ln):
         L.gpt2_tune_prefill_fused(1)
         L.gpt2_tune_gemm_ln_force(-1)
         L.gpt2_tune_prefill_persistent(-1)
+        L.gpt2_tune_prefill_lnfold(-1)
         if backend == "int8":
             L.gpt2_quant_free(C.byref(model.q))
             model.q = None

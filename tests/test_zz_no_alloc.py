@@ -1,9 +1,10 @@
 """gpt2_forward_noalloc (the forward with its activations in a static device array, no allocation)
 against gpt2_forward_cuda (the same forward on an allocated GPT2ScratchGPU).  The no-allocation entry
-point runs the per-op launch sequence (the persistent trunk kernel allocates its arena on first use),
-so it matches gpt2_forward_cuda with that kernel switched off (the default) bit for bit -- all logits
-rows, the final LayerNorm, every layer's residual stream and the K/V cache it fills -- and
-gpt2_forward_cuda with the persistent kernel switched on within the fp16 gates.  Two calls in a row, the second with fewer tokens
+point runs the per-op launch sequence unfolded (the persistent trunk kernel allocates its arena, and
+the LayerNorm fold its per-weights constants, on first use), so it matches gpt2_forward_cuda with
+both switched off bit for bit -- all logits rows, the final LayerNorm, every layer's residual stream
+and the K/V cache it fills -- and gpt2_forward_cuda with the fold on (the default), or with the
+persistent kernel on, within the fp16 gates.  Two calls in a row, the second with fewer tokens
 (the array keeps the first call's contents), for the fp16 and the INT8 backend; and a call past the
 static limit is refused with an error and writes nothing.  The property itself: across a call, the
 library's allocation count (every device allocation goes through gpt2_dmalloc) and the device's free
@@ -64,13 +65,26 @@ def test_forward_noalloc_matches_forward(pkg, L, synth, model, backend):
             ids = synth.token_ids(T, seed=T + 3)
             print(f"forward_noalloc backend={backend} T={T}", flush=True)
             got = run(pkg, L, model, backend, ids, noalloc=True)
+            # the no-allocation entry point runs the unfolded launch sequence (the LayerNorm fold builds
+            # per-weights constants on first use): bit for bit against gpt2_forward_cuda with the
+            # fold off, to the fp16 bar against it with the fold on
             L.gpt2_tune_prefill_persistent(0)
+            L.gpt2_tune_prefill_lnfold(0)
             try:
                 ref = run(pkg, L, model, backend, ids, noalloc=False)
             finally:
                 L.gpt2_tune_prefill_persistent(-1)
+                L.gpt2_tune_prefill_lnfold(-1)
             for name, a, b in zip(("logits", "final_ln", "blocks", "kv"), got, ref):
                 assert np.array_equal(a, b), f"{backend} T={T}: {name} differs in {np.count_nonzero(a != b)} elements"
+            L.gpt2_tune_prefill_persistent(0)
+            try:
+                folded = run(pkg, L, model, backend, ids, noalloc=False)
+            finally:
+                L.gpt2_tune_prefill_persistent(-1)
+            for name, a, b in zip(("logits", "final_ln", "blocks"), got, folded):
+                fa, fb = oracle.f16_to_f32(a).astype(np.float64), oracle.f16_to_f32(b).astype(np.float64)
+                assert np.abs(fa - fb).max() / (np.abs(fb).max() + 1e-9) <= 1e-2, (backend, T, name, "lnfold")
             L.gpt2_tune_prefill_persistent(1)
             try:
                 pers = run(pkg, L, model, backend, ids, noalloc=False)
