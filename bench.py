@@ -7,7 +7,13 @@ Headline (`value`): fp16 prefill GEMM TFLOP/s at P=512 -- one step is the prefil
 resident in HBM before the timed region; timing is hipEvents on the launch stream around K steps.
 
 Also reported in the same JSON line:
-  roofline      the GEMM kernel with the largest share of the step, against 2500 TFLOP/s fp16 MFMA
+  step_stats    one hipEvent pair per step: mean (= ms_per_step), median and [min, max], with the
+                TFLOP/s at each
+  clock         the gfx clock amd-smi reports while the step runs back to back (median, [min, max])
+  launch_floor_us  an empty kernel launched back to back (the per-launch floor of this box)
+  roofline      the GEMM kernel with the largest share of the step, against 2500 TFLOP/s fp16 MFMA:
+                `achieved` from its rocprof mean in profiles/gemm_prefill_p512_kernel_trace.json
+                (the primary kernel time), this run's hipEvent launch average beside it
   gemm_set_graph_replay  the same step captured once as a hipGraph and replayed (no faster: the
                 gap between dependent launches is the same inside a graph)
   gemv_int8     INT8 decode GEMV GB/s per trunk shape, cold (rotating > 512 MB of weight copies,
@@ -23,10 +29,16 @@ Also reported in the same JSON line:
                 line): legs above it are listed as suspicious
   attention_prefill  causal MFMA prefill attention per launch at T=512 and T=1024 (12 heads x 64)
   forward_t64   config 1 on the GPU: the fp16 forward at T=64 with logits for all 64 rows
+  prefill       the whole prefill at P=512 (fp16 and INT8 trunk weights) and at P=128 with the
+                LayerNorm fold at its default and off; prefill_trunk_gemm_tflops = the trunk's
+                86.97 GFLOP / the fp16 P=512 forward (a lower bound: attention, LayerNorms, head row
+                in the denominator)
   decode        GPT-2-124M decode tok/s @ctx=512: INT8 trunk + fp16 head, one hipGraph replay per
                 token, after a P=512 prefill (the prefill itself is timed too); plus the mean over
                 the 511-step greedy run, and (decode.cold) the same step with its weights cold:
                 four uploads of the model stepped round robin, 650 MB of weights past the 256 MB MALL
+  decode_fp16_vs_int8  the persistent step with fp16 and with INT8 trunk weights at ctx 128, 512 and
+                1023, warm and cold, the fp16 and INT8 48-GEMV chains, and the INT8/fp16 ratios
   cpu_baseline  the reference's own cpu/forward_cpu.c matmul (oracle/_ref, if built) or the oracle
                 restatement, on the same four GEMM shapes, on this host's cores
   cpu_forward_t64  config 1 on the CPU: the reference's forward at T=64 with logits_all (median of
@@ -591,6 +603,72 @@ def bench_forward_t64(B, reps=20):
     scr.free()
     return {"T": T, "logits_all": True, "backend": "flash (fp16)", "gflop": 15.89,
             "ms_median": round(float(np.median(ms)), 4), "ms_min_max": [round(min(ms), 4), round(max(ms), 4)]}
+
+
+def bench_prefill(B, reps=30):
+    """The whole prefill (gpt2_prefill_fill_cache: embedding, 12 layers with attention and the K/V
+    fill, final LayerNorm, last-row logits) at P=512 with fp16 and with INT8 trunk weights, and at
+    P=128 with the LayerNorm fold at its default (on there) and off; one hipEvent pair per forward
+    on the library's stream, median and [min, max] of `reps` forwards after 3 untimed ones.
+    prefill_trunk_gemm_tflops = the 48 trunk GEMMs' 86.97 GFLOP / the fp16 P=512 forward: attention,
+    LayerNorms and the head row sit in the denominator, so it is a lower bound on the trunk rate."""
+    pkg, L = B.pkg, B.L
+    synth = importlib.import_module("bare_metal_gpt2_amd.synth")
+    hip = C.CDLL("libamdhip64.so")
+    for fn in ("hipEventCreate", "hipEventRecord", "hipEventElapsedTime", "hipEventDestroy"):
+        getattr(hip, fn).restype = C.c_int
+    stream = C.c_void_p(L.gpt2_get_stream())
+
+    def run(model, backend, T, lnfold=-1):
+        kv, scr = pkg.KVCache(T), pkg.Scratch(T)
+        d_ids = B.dev(synth.token_ids(T, seed=1234))
+        logits = B.empty(VOCAB * 2)
+        caps = pkg.GPT2CapsGPU()
+        caps.logits, caps.logits_all = logits.ptr, 0
+        be = pkg.backend(backend)
+        L.gpt2_tune_prefill_lnfold(lnfold)
+        ev = [(C.c_void_p(), C.c_void_p()) for _ in range(reps)]
+        for a, b in ev:
+            hip.hipEventCreate(C.byref(a))
+            hip.hipEventCreate(C.byref(b))
+        try:
+            for _ in range(3):
+                L.gpt2_prefill_fill_cache(be, C.byref(model.gpu), C.byref(kv.kv), d_ids.ptr, T, C.byref(scr.s),
+                                          C.byref(caps))
+            for a, b in ev:
+                hip.hipEventRecord(a, stream)
+                L.gpt2_prefill_fill_cache(be, C.byref(model.gpu), C.byref(kv.kv), d_ids.ptr, T, C.byref(scr.s),
+                                          C.byref(caps))
+                hip.hipEventRecord(b, stream)
+            L.gpt2_sync()
+            pkg.check(f"prefill {backend} T={T}")
+            ms = []
+            for a, b in ev:
+                t = C.c_float()
+                hip.hipEventElapsedTime(C.byref(t), a, b)
+                ms.append(t.value)
+        finally:
+            L.gpt2_tune_prefill_lnfold(-1)
+            for a, b in ev:
+                hip.hipEventDestroy(a)
+                hip.hipEventDestroy(b)
+            kv.free()
+            scr.free()
+        return {"ms_median": round(float(np.median(ms)), 4), "ms_min_max": [round(min(ms), 4), round(max(ms), 4)]}
+
+    model = pkg.Model(seeded_body())
+    out = {"fp16_p512": run(model, "flash", 512), "fp16_p128": run(model, "flash", 128),
+           "fp16_p128_lnfold_off": run(model, "flash", 128, 0)}
+    model.quantize()
+    out["int8_p512"] = run(model, "int8", 512)
+    out["int8_p128"] = run(model, "int8", 128)
+    out["int8_p128_lnfold_off"] = run(model, "int8", 128, 0)
+    model.free()
+    trunk_flop = N_LAYER * sum(2.0 * M_PREFILL * N * K for _, N, K in GEMM_SET)
+    out["prefill_trunk_gemm_tflops"] = round(trunk_flop / (out["fp16_p512"]["ms_median"] * 1e-3) / 1e12, 2)
+    for w in ("fp16", "int8"):
+        out[f"{w}_p128_lnfold_speedup"] = round(out[f"{w}_p128_lnfold_off"]["ms_median"] / out[f"{w}_p128"]["ms_median"], 3)
+    return out
 
 
 def cpu_forward_t64():
@@ -1229,6 +1307,9 @@ def main():
         out["forward_t64"] = bench_forward_t64(B)
         B.keep.clear()
         log(f"forward T=64: {out['forward_t64']}")
+        out["prefill"] = bench_prefill(B)
+        B.keep.clear()
+        log(f"prefill: {out['prefill']}")
         if not args.no_decode:
             out["decode"] = bench_decode(B)
             B.keep.clear()
