@@ -145,7 +145,7 @@ def f16(rng, shape, std):
 
 
 # ------------------------------------------------------------------------------ prefill GEMM set
-def bench_gemm_set(B, steps, warmup):
+def bench_gemm_set(B, steps, warmup, clock=True):
     rng = np.random.default_rng(1234)
     L = B.L
     X = B.dev(f16(rng, (M_PREFILL, 768), 1.0))
@@ -167,7 +167,10 @@ def bench_gemm_set(B, steps, warmup):
                   "tflops_median": tf(float(np.median(per_ms))), "tflops_at_min_max_ms": [tf(min(per_ms)), tf(max(per_ms))],
                   "timing": "one hipEvent pair per step on the launch stream (steps share their boundary events); "
                             "ms_per_step and value use the mean"}
-    clock = sustained_clock(B, ops)
+    if clock:
+        clock = sustained_clock(B, ops)
+    else:
+        clock = {"sclk_mhz": None, "method": "skipped (--no-clock)"}
     ms_graph = B.run_ops_graph(ops, warmup, steps)
     # Per-kernel launch durations for the roofline, under the step's own conditions: each shape's
     # 12 layer GEMMs (distinct weights, so the weights are not L2-resident) back to back.
@@ -1210,6 +1213,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-clock", action="store_true",
+                    help="skip the amd-smi clock sampler; use it under rocprofv3, whose preload would make the "
+                         "amd-smi child initialise the GPU before its launcher execs python")
     ap.add_argument("--no-extras", action="store_true", help="only the headline GEMM set")
     ap.add_argument("--no-decode", action="store_true", help="skip the graph-replayed decode leg")
     ap.add_argument("--gemv-only", action="store_true",
@@ -1265,7 +1271,7 @@ def main():
     if args.decode_only:
         print(json.dumps({"decode": bench_decode(B, steady_reps=32, greedy=False)}), flush=True)
         return
-    flops_step, ms_step, shapes, roofline, ms_graph, step_stats, clock = bench_gemm_set(B, args.steps, args.warmup)
+    flops_step, ms_step, shapes, roofline, ms_graph, step_stats, clock = bench_gemm_set(B, args.steps, args.warmup, not args.no_clock)
     value = flops_step / (ms_step * 1e-3) / 1e12
     log(f"prefill GEMM set: {ms_step * 1e3:.1f} us/step -> {value:.1f} TFLOP/s; steps {step_stats}; clock {clock}")
     log(f"per shape {shapes}")
