@@ -197,3 +197,78 @@ def test_lnfold_constants_follow_weights(pkg, L, synth):
             assert_close(got, ref)
         finally:
             m.free()
+
+
+def hip_runtime():
+    h = C.CDLL("libamdhip64.so")
+    for name in ("hipStreamCreate", "hipStreamBeginCapture", "hipStreamEndCapture", "hipGraphInstantiate",
+                 "hipGraphLaunch", "hipStreamSynchronize", "hipGraphExecDestroy", "hipGraphDestroy",
+                 "hipStreamDestroy"):
+        getattr(h, name).restype = C.c_int
+    return h
+
+
+@pytest.mark.parametrize("warm", [True, False])
+def test_lnfold_under_graph_capture(pkg, L, synth, warm):
+    """gpt2_forward_cuda at T = 64 (inside the fold's default range) captured into a HIP graph on a
+    stream of its own.  warm: the weights' fold constants exist (an eager call built them), so the
+    captured forward runs folded (47 sites) and every replay equals the eager folded call bit for bit.
+    cold: fresh weights, so the constants would need an allocation, which is not made under capture;
+    the captured forward runs unfolded (0 sites) and every replay equals the eager unfolded call.
+    Between the replays the eager forward runs on other ids at the default (in the cold case that
+    builds the constants; the instantiated graph is unaffected)."""
+    hip = hip_runtime()
+    m = pkg.Model(synth.make_body(seed=21 if warm else 22, plain=False))
+    T = 64
+    ids, other = synth.token_ids(T, seed=61), synth.token_ids(T, seed=62)
+    d_ids, d_other = pkg.Dev.from_numpy(np.asarray(ids, np.int32)), pkg.Dev.from_numpy(np.asarray(other, np.int32))
+    scr = pkg.Scratch(T)
+    logits, fin = pkg.Dev(T * V * 2), pkg.Dev(T * E * 2)
+    caps = pkg.GPT2CapsGPU()
+    caps.logits, caps.logits_all, caps.final_ln = logits.ptr, 1, fin.ptr
+    be = pkg.backend("flash")
+
+    def eager(d, lnfold):
+        L.gpt2_tune_prefill_lnfold(lnfold)
+        try:
+            L.gpt2_forward_cuda(be, C.byref(m.gpu), d.ptr, T, C.byref(scr.s), C.byref(caps))
+            L.gpt2_sync()
+            pkg.check("eager forward")
+            sites = L.gpt2_tune_prefill_lnfold_sites()
+        finally:
+            L.gpt2_tune_prefill_lnfold(-1)
+        return (logits.numpy(np.uint16, (T * V,)).copy(), fin.numpy(np.uint16, (T * E,)).copy()), sites
+
+    stream, graph, exe = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    try:
+        print(f"lnfold capture warm={warm}", flush=True)
+        ref, sites = eager(d_ids, -1 if warm else 0)
+        assert sites == (SITES if warm else 0)
+        assert hip.hipStreamCreate(C.byref(stream)) == 0
+        L.gpt2_set_stream(stream)
+        assert hip.hipStreamBeginCapture(stream, 1) == 0          # hipStreamCaptureModeThreadLocal
+        L.gpt2_forward_cuda(be, C.byref(m.gpu), d_ids.ptr, T, C.byref(scr.s), C.byref(caps))
+        captured_sites = L.gpt2_tune_prefill_lnfold_sites()
+        assert hip.hipStreamEndCapture(stream, C.byref(graph)) == 0
+        pkg.check("capture")
+        assert captured_sites == (SITES if warm else 0)
+        assert hip.hipGraphInstantiate(C.byref(exe), graph, None, None, 0) == 0
+        for r in range(3):
+            eager(d_other, -1)
+            L.gpt2_memset(logits.ptr, 0, T * V * 2)
+            assert hip.hipGraphLaunch(exe, stream) == 0
+            assert hip.hipStreamSynchronize(stream) == 0
+            pkg.check("replay")
+            got = (logits.numpy(np.uint16, (T * V,)), fin.numpy(np.uint16, (T * E,)))
+            for name, a, b in zip(("logits", "final_ln"), got, ref):
+                assert np.array_equal(a, b), f"replay {r}: {name} differs in {np.count_nonzero(a != b)} elements"
+    finally:
+        L.gpt2_set_stream(None)
+        if exe:
+            hip.hipGraphExecDestroy(exe)
+        if graph:
+            hip.hipGraphDestroy(graph)
+        if stream:
+            hip.hipStreamDestroy(stream)
+        scr.free()
+        m.free()
