@@ -228,8 +228,9 @@ static void capcpy(gpt2_half *dst, const gpt2_half *src, size_t n) { gpt2_d2d(ds
 // When the backend's matmul, gelu, add and attention slots are this library's, the prefill runs
 // fused: gelu in the fc GEMM's epilogue, the residual adds in the attn-proj and mlp-proj epilogues,
 // the K/V cache fill inside the attention launch -- 5 launches per layer instead of 9, each result
-// bit-identical to the unfused sequence (same fp16 rounding points).  Other backends, and shapes the
-// fused GEMM does not take, run the reference's sequence (cuda/forward_cuda.cu:90-106).
+// bit-identical to the unfused sequence (same fp16 rounding points; the LayerNorm fold below, taken
+// by default for short prompts, is the exception).  Other backends, and shapes the fused GEMM does
+// not take, run the reference's sequence (cuda/forward_cuda.cu:90-106).
 static bool g_prefill_fused = true;   // gpt2_tune_prefill_fused (tests compare both sequences)
 static bool fused_prefill_ok(const GPT2Backend *be) {
     return g_prefill_fused && be->matmul == gpt2_matmul_tiled &&
