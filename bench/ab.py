@@ -14,6 +14,7 @@ WORKLOAD (one sample = the mean over a short burst, microseconds):
   gemm_shape     one trunk shape, 12 layers of distinct weights back to back (knob shape=qkv|...)
   head_gemm      the tied head as a GEMM, [512x768] . [768x50257]^T
   gemv_chain     the 48 trunk GEMVs of one decode step, distinct weights (knob dtype=int8|fp16)
+  gemv           one trunk GEMV per launch, us per launch (knobs shape, dtype, cold=1|0, gemv_cfg)
   decode_step    one persistent (or multi-kernel) decode step of GPT-2-124M, re-pinned at a position
   prefill        gpt2_prefill_fill_cache at T tokens, host-timed around a device sync
   empty          an empty kernel back to back (the launch floor)
@@ -23,7 +24,8 @@ SPEC: comma-separated key=value knobs; an empty SPEC ("") is the library's defau
                  a side with lib= runs in worker subprocesses, alternated with the other side's
   gemm_cfg=C     force GEMM tile config C for every call (gpt2_tune_gemm_force; -1 = the picks)
   prefill_persistent=0|1, lnfold=0|1 (the prefill's LayerNorm fold), backend=int8|gemv|flash, pos=P, T=T, mode=persistent|multi,
-  dtype=int8|fp16, shape=qkv|attn_proj|fc|mlp_proj, big_alloc=GiB (allocate, touch and free that
+  gemv_cfg=C     force GEMV config C (gemv workload; -1 = the library's pick),
+  dtype=int8|fp16, shape=qkv|attn_proj|fc|mlp_proj, cold=1|0, big_alloc=GiB (allocate, touch and free that
   much device memory before the workload's own buffers, as bench.py's measured peaks leg does)
 
 Examples:
@@ -197,6 +199,39 @@ def make_gemv_chain(env, knobs):
     return OpsWorkload(env, ops, burst=20)
 
 
+def make_gemv(env, knobs):
+    """One trunk GEMV (knob shape), INT8 or fp16 (knob dtype); cold (knob cold=1, the default): the
+    launches rotate over >= 600 MB of weight copies, so each streams from HBM; gemv_cfg=C forces
+    GEMV config C (the harness's kind 256 + C), -1 the library's pick."""
+    rng = np.random.default_rng(4321)
+    N, K = SHAPES[knobs.get("shape", "mlp_proj")]
+    fp16 = knobs.get("dtype", "int8") == "fp16"
+    cold = int(knobs.get("cold", 1)) != 0
+    cfg = int(knobs.get("gemv_cfg", -1))
+    x = env.dev(f16(rng, K, 1.0))
+    y = env.empty(N * 2)
+    b = env.dev(f16(rng, N, 0.01))
+    nb = N * K * (2 if fp16 else 1)
+    copies = max(1, int(600e6 // nb) + 1) if cold else 1
+    big = env.empty(copies * nb)
+    w_host = f16(rng, (N, K), 0.02) if fp16 else rng.integers(-127, 128, (N, K), dtype=np.int8)
+    env.L.gpt2_h2d(big.ptr, w_host.ctypes.data, nb)
+    env.L.gpt2_sync()
+    s = None if fp16 else env.dev(np.full(N, 1e-3, np.float32))
+    for r in range(1, copies):
+        env.L.gpt2_d2d(big.ptr + r * nb, big.ptr, nb)
+    env.L.gpt2_sync()
+    kind = 256 + cfg if cfg >= 0 else (2 if fp16 else 3)
+    ops = [env.harness.GPT2BenchOp(kind, y.ptr, x.ptr, big.ptr + r * nb, s.ptr if s is not None else None, b.ptr, 1,
+                                   N, K) for r in range(copies)]
+
+    class GemvWorkload(OpsWorkload):
+        def sample(self, knobs):
+            return OpsWorkload.sample(self, knobs) / copies   # us per launch
+
+    return GemvWorkload(env, ops, burst=3 if cold else 300)
+
+
 class EmptyWorkload:
     def __init__(self, env, knobs):
         self.env = env
@@ -312,6 +347,8 @@ def make_workload(env, name, knobs):
         return make_gemm_set(env, knobs, int8=True)
     if name == "gemm_shape":
         return make_gemm_set(env, knobs, int8=knobs.get("dtype") == "int8", only=knobs.get("shape", "mlp_proj"))
+    if name == "gemv":
+        return make_gemv(env, knobs)
     if name == "head_gemm":
         return make_head_gemm(env, knobs)
     if name == "gemv_chain":
@@ -371,7 +408,7 @@ def main():
         env = Env()
         wa = make_workload(env, args.workload, ka)
         # the same workload object serves both sides unless their buffers would differ
-        same = all(ka.get(k) == kb.get(k) for k in ("big_alloc", "dtype", "shape"))
+        same = all(ka.get(k) == kb.get(k) for k in ("big_alloc", "dtype", "shape", "gemv_cfg", "cold"))
         wb = wa if same else make_workload(env, args.workload, kb)
         wa.sample(ka)
         wb.sample(kb)

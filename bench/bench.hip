@@ -8,8 +8,8 @@
 
 extern "C" {
 
-// Tuning hooks of libgpt2amd.so (csrc/gemm.hip): one GEMM on a fixed tile config, the fused-epilogue
-// GEMM, the LayerNorm-panel GEMM.  Weak, so this harness also loads against an older build of the
+// Tuning hooks of libgpt2amd.so (csrc/gemm.hip, csrc/gemv.hip): one GEMM on a fixed tile config, the
+// fused-epilogue GEMM, the LayerNorm-panel GEMM, one GEMV on a fixed config.  Weak, so this harness also loads against an older build of the
 // library that lacks them (bench/ab_build.sh); the ops that need a missing hook record an error.
 __attribute__((weak)) void gpt2_tune_gemm_run(int cfg, gpt2_half *C, const gpt2_half *A, const void *W,
                                               const float *Ws, const gpt2_half *bias, int M, int N, int K);
@@ -19,6 +19,8 @@ __attribute__((weak)) int gpt2_tune_gemm_fused(gpt2_half *C, const gpt2_half *A,
 __attribute__((weak)) int gpt2_tune_gemm_ln(int cfg, gpt2_half *C, const gpt2_half *X, const gpt2_half *g,
                                             const gpt2_half *b, const void *W, const float *Ws, const gpt2_half *bias,
                                             int M, int N, int K, int epi);
+__attribute__((weak)) void gpt2_tune_gemv_run(int cfg, gpt2_half *C, const gpt2_half *A, const void *W,
+                                              const float *Ws, const gpt2_half *bias, int N, int K);
 static int missing_hook = 0;
 
 // One timed operation: kind 0 = fp16 GEMM (gpt2_matmul_tiled), 1 = INT8 GEMM (gpt2_matmul_int8),
@@ -29,7 +31,8 @@ static int missing_hook = 0;
 // gelu fused (gpt2_tune_gemm_fused epi 1), 9 = gelu in place (gpt2_gelu, M*N elements), 16 + c = the GEMM
 // on tile config c (gpt2_tune_gemm_run; INT8 weights when Ws is not NULL), for sweeps that mix
 // configs in one step, 64 + c = the LayerNorm-panel GEMM on LN config c (gpt2_tune_gemm_ln, K = 768,
-// the bias standing in for gamma and beta: a timing form only).
+// the bias standing in for gamma and beta: a timing form only), 256 + c = the GEMV on config c
+// (gpt2_tune_gemv_run; INT8 codes when Ws is not NULL).
 typedef struct {
     int kind;
     gpt2_half *C;
@@ -59,7 +62,10 @@ static void run_op(const GPT2BenchOp &o) {
             break;
         case 9: gpt2_gelu(o.C, (size_t)o.M * o.N); break;
         default:
-            if (o.kind >= 64 && gpt2_tune_gemm_ln)   // LayerNorm-panel GEMM on LN config kind - 64; the bias doubles as gamma and beta
+            if (o.kind >= 256) {
+                if (gpt2_tune_gemv_run) gpt2_tune_gemv_run(o.kind - 256, o.C, o.A, o.W, o.Ws, o.bias, o.N, o.K);
+                else missing_hook = 1;
+            } else if (o.kind >= 64 && gpt2_tune_gemm_ln)   // LayerNorm-panel GEMM on LN config kind - 64; the bias doubles as gamma and beta
                 gpt2_tune_gemm_ln(o.kind - 64, o.C, o.A, o.bias, o.bias, o.W, o.Ws, o.bias, o.M, o.N, o.K, 0);
             else if (o.kind < 64 && gpt2_tune_gemm_run) gpt2_tune_gemm_run(o.kind - 16, o.C, o.A, o.W, o.Ws, o.bias, o.M, o.N, o.K);
             else missing_hook = 1;

@@ -22,7 +22,7 @@ class GPT2BenchOp(C.Structure):
     4 causal prefill attention (C = att, A = qkv, M = T), 5 LayerNorm (C = out, A = x, W = gamma,
     bias = beta, M rows of K), 6 GEMM + residual in place (C += A.W^T + b), 7 residual add (C += A,
     M*N elements), 8 GEMM + gelu, 9 gelu in place (M*N elements), 16 + c the GEMM on tile config c
-    (INT8 when Ws is set)."""
+    (INT8 when Ws is set), 256 + c the GEMV on config c (INT8 when Ws is set)."""
     _fields_ = [("kind", C.c_int), ("C", _vp), ("A", _vp), ("W", _vp), ("Ws", _vp), ("bias", _vp),
                 ("M", C.c_int), ("N", C.c_int), ("K", C.c_int)]
 
