@@ -14,7 +14,8 @@ WORKLOAD (one sample = the mean over a short burst, microseconds):
   gemm_shape     one trunk shape, 12 layers of distinct weights back to back (knob shape=qkv|...)
   head_gemm      the tied head as a GEMM, [512x768] . [768x50257]^T
   gemv_chain     the 48 trunk GEMVs of one decode step, distinct weights (knob dtype=int8|fp16)
-  gemv           one trunk GEMV per launch, us per launch (knobs shape, dtype, cold=1|0, gemv_cfg)
+  gemv           one GEMV per launch, us per launch (knobs shape (a trunk shape or head), dtype,
+                 cold=1|0, gemv_cfg)
   decode_step    one persistent (or multi-kernel) decode step of GPT-2-124M, re-pinned at a position
   prefill        gpt2_prefill_fill_cache at T tokens, host-timed around a device sync
   empty          an empty kernel back to back (the launch floor)
@@ -204,7 +205,8 @@ def make_gemv(env, knobs):
     launches rotate over >= 600 MB of weight copies, so each streams from HBM; gemv_cfg=C forces
     GEMV config C (the harness's kind 256 + C), -1 the library's pick."""
     rng = np.random.default_rng(4321)
-    N, K = SHAPES[knobs.get("shape", "mlp_proj")]
+    name = knobs.get("shape", "mlp_proj")
+    N, K = (50257, 768) if name == "head" else SHAPES[name]
     fp16 = knobs.get("dtype", "int8") == "fp16"
     cold = int(knobs.get("cold", 1)) != 0
     cfg = int(knobs.get("gemv_cfg", -1))
