@@ -1,7 +1,7 @@
 #!/usr/bin/env python
-"""Summaries of rocprofv3 counter runs (`--pmc`, *_counter_collection.csv) of the prefill GEMM set, per
-GEMM shape.  The shape of each kernel comes from the bench line the profiled run printed (its
-`gemm_shapes`: every trunk config serves one shape of the set).
+"""Summaries of rocprofv3 counter runs (`--pmc`, *_counter_collection.csv): the prefill GEMM set per GEMM
+shape (the shape of each kernel comes from the bench line the profiled run printed, its
+`gemm_shapes`: every trunk config serves one shape of the set), and the decode GEMV legs.
 
   python bench/pmc_summary.py mfma PMC.csv RUN.json [--bench BENCH.json] [--clock-mhz 2400]
       SQ_INSTS_VALU_MFMA_MOPS_F16 (units of 512 FLOP), SQ_VALU_MFMA_BUSY_CYCLES (summed over the 1024
@@ -12,6 +12,10 @@ GEMM shape.  The shape of each kernel comes from the bench line the profiled run
       FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each scaled by what the same counter reads for the
       harness's copy kernel of N bytes (k_copy16, `bench.py --copy-probe N`), against the algorithmic
       bytes (A, W and bias read, C written once).  --json writes what bench.py's roofline reads.
+  python bench/pmc_summary.py gemv FETCH.csv WRITE.csv TRACE.csv [--copy-bytes N]
+      the decode GEMV legs (`bench.py --gemv-only`): per k_gemv kernel and grid, the shape from its
+      template arguments and grid (N rows of K), FETCH_SIZE / WRITE_SIZE (median per dispatch),
+      scaled, against the algorithmic bytes, with the kernel-trace median duration.
 """
 from __future__ import annotations
 
@@ -71,6 +75,70 @@ def counters(path):
 
 def shape_label(x):
     return f"{LABEL.get(x['gemm'], x['gemm'])} {x['M']}x{x['N']}x{x['K']}"
+
+
+GEMV_LEGS = {(2304, 768): "QKV", (768, 768): "attn-proj", (3072, 768): "fc", (768, 3072): "mlp-proj",
+             (50257, 768): "tied head"}
+
+
+def gemv_shape(name, grid, wg):
+    """(N, K, INT8) of a k_gemv<LPR, CPL, U, QW, ...> dispatch: rows per work-group (64/LPR) * U *
+    (wg/64), K = LPR * CPL * 16 bytes of weights per row; N = the rows the grid covers (a multiple of
+    the rows per work-group: the last one may be partial, so N is matched to the known legs)."""
+    import re
+    m = re.search(r"k_gemv<(\d+), (\d+), (\d+), (true|false)", name)
+    if not m:
+        return None
+    lpr, cpl, u, qw = int(m.group(1)), int(m.group(2)), int(m.group(3)), m.group(4) == "true"
+    rows_wg = (64 // lpr) * u * (wg // 64)
+    k = lpr * cpl * 16 // (1 if qw else 2)
+    cover = (grid // wg) * rows_wg
+    for (n, kk) in GEMV_LEGS:
+        if kk == k and cover - rows_wg < n <= cover:
+            return n, k, qw
+    return None
+
+
+def cmd_gemv(a):
+    def rows(path):
+        with open(path, newline="") as f:
+            return list(csv.DictReader(f))
+    fet, wri, tr = rows(a.fetch), rows(a.write), rows(a.trace)
+    def copy_val(rs, counter):
+        v = [float(r["Counter_Value"]) for r in rs if short(r["Kernel_Name"]) == "k_copy16" and r["Counter_Name"] == counter]
+        return statistics.fmean(v)
+    kib = a.copy_bytes / 1024
+    fs, ws = kib / copy_val(fet, "FETCH_SIZE"), kib / copy_val(wri, "WRITE_SIZE")
+    def by_leg(rs, key_grid, key_wg, val):
+        out = {}
+        for r in rs:
+            nm = short(r["Kernel_Name"])
+            if "k_gemv<" not in nm:
+                continue
+            sh = gemv_shape(nm, int(r[key_grid]), int(r[key_wg]))
+            if sh:
+                out.setdefault((nm, sh), []).append(val(r))
+        return out
+    f = by_leg(fet, "Grid_Size", "Workgroup_Size", lambda r: float(r["Counter_Value"]))
+    w = by_leg(wri, "Grid_Size", "Workgroup_Size", lambda r: float(r["Counter_Value"]))
+    t = by_leg(tr, "Grid_Size_X", "Workgroup_Size_X", lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    print(f"Calibration: `k_copy16` copying {a.copy_bytes} B reads FETCH_SIZE = {kib / fs:.1f} KiB and WRITE_SIZE = "
+          f"{kib / ws:.1f} KiB, so the scale factors are {fs:.3f} (fetch) and {ws:.3f} (write).\n")
+    print("| leg | kernel | dispatches | FETCH_SIZE KiB (median) | WRITE_SIZE KiB | scaled bytes | algorithmic bytes "
+          "| ratio | kernel us (trace median) |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    order = sorted(f, key=lambda k: (not k[1][2], k[1][0] == 50257, list(GEMV_LEGS).index(k[1][:2])))
+    for key in order:
+        nm, (n, k, qw) = key
+        fk, wk = statistics.median(f[key]), statistics.median(w.get(key, [0.0]))
+        scaled = fk * fs * 1024 + wk * ws * 1024
+        head = n == 50257
+        bias = 0 if head else 2 * n
+        algo = (n * k + 4 * n + 2 * k + 2 * n + bias) if qw else (2 * n * k + 2 * k + 2 * n + bias)
+        us = statistics.median(t[key]) if key in t else float("nan")
+        leg = f"{'INT8' if qw else 'fp16'} {GEMV_LEGS[(n, k)]} {k}x{n}"
+        print(f"| {leg} | `{nm}` | {len(f[key])} | {fk:.1f} | {wk:.2f} | {scaled / 1e6:.3f} MB | {algo / 1e6:.3f} MB | "
+              f"{scaled / algo:.3f} | {us:.2f} |")
 
 
 def cmd_mfma(a):
@@ -142,6 +210,11 @@ def main():
     p.add_argument("run", help="stdout of the profiled bench.py run (its JSON line)")
     p.add_argument("--bench", default=None, help="an untraced bench line, for the per-launch times")
     p.add_argument("--clock-mhz", type=float, default=2400.0)
+    p = sub.add_parser("gemv")
+    p.add_argument("fetch")
+    p.add_argument("write")
+    p.add_argument("trace")
+    p.add_argument("--copy-bytes", type=int, default=268435456)
     p = sub.add_parser("traffic")
     p.add_argument("fetch")
     p.add_argument("write")
@@ -150,7 +223,7 @@ def main():
     p.add_argument("--json", default=None)
     p.add_argument("--source", default=None)
     a = ap.parse_args()
-    {"mfma": cmd_mfma, "traffic": cmd_traffic}[a.cmd](a)
+    {"mfma": cmd_mfma, "traffic": cmd_traffic, "gemv": cmd_gemv}[a.cmd](a)
 
 
 if __name__ == "__main__":
