@@ -89,6 +89,7 @@ class Env:
         self.pkg = __graft_entry__.load_package()
         self.harness = importlib.import_module("harness")
         if libdir:
+            libdir = os.path.abspath(libdir)      # dlopen reads a bare relative name as a search name
             self.pkg.LIB_PATH = os.path.join(libdir, "libgpt2amd.so")
             self.harness.LIB_PATH = os.path.join(libdir, "libgpt2bench.so")
             raw = C.CDLL(self.pkg.LIB_PATH)
