@@ -28,6 +28,8 @@ SPEC: comma-separated key=value knobs; an empty SPEC ("") is the library's defau
   gemv_cfg=C     force GEMV config C (gemv workload; -1 = the library's pick),
   dtype=int8|fp16, shape=qkv|attn_proj|fc|mlp_proj, cold=1|0, big_alloc=GiB (allocate, touch and free that
   much device memory before the workload's own buffers, as bench.py's measured peaks leg does)
+  epi=gelu|resid  gemm_shape / gemm_set: the fused-epilogue GEMM the prefill runs (gelu after the
+                 product, or the residual added in place) instead of the plain one
 
 Examples:
   python bench/ab.py gemm_set --a "" --b gemm_cfg=12
@@ -155,7 +157,13 @@ def make_gemm_set(env, knobs, int8=False, only=None):
     H = env.harness
     X = env.dev(f16(rng, (512, 768), 1.0))
     Xf = env.dev(f16(rng, (512, 3072), 1.0))
-    outs = {k: env.empty(512 * SHAPES[k][0] * 2) for k in ORDER}
+    # plain GEMM (harness kind 0 fp16 / 1 INT8), or the fused epilogue: 8 gelu, 6 residual added into C
+    # (C then starts as data, not as whatever the allocation held)
+    epi = {"gelu": 8, "resid": 6}.get(knobs.get("epi", ""), None)
+    if epi is None:
+        outs = {k: env.empty(512 * SHAPES[k][0] * 2) for k in ORDER}
+    else:
+        outs = {k: env.dev(f16(np.random.default_rng(99), (512, SHAPES[k][0]), 1.0)) for k in ORDER}
     ops = []
     for _ in range(12):
         for k in ORDER if only is None else [only]:
@@ -165,10 +173,10 @@ def make_gemm_set(env, knobs, int8=False, only=None):
             if int8:
                 W = env.dev(rng.integers(-127, 128, (N, K), dtype=np.int8))
                 s = env.dev((rng.random(N, dtype=np.float32) * np.float32(2e-4) + np.float32(1e-4)))
-                ops.append(H.GPT2BenchOp(1, outs[k].ptr, A.ptr, W.ptr, s.ptr, b.ptr, 512, N, K))
+                ops.append(H.GPT2BenchOp(epi or 1, outs[k].ptr, A.ptr, W.ptr, s.ptr, b.ptr, 512, N, K))
             else:
                 W = env.dev(f16(rng, (N, K), 0.02))
-                ops.append(H.GPT2BenchOp(0, outs[k].ptr, A.ptr, W.ptr, None, b.ptr, 512, N, K))
+                ops.append(H.GPT2BenchOp(epi or 0, outs[k].ptr, A.ptr, W.ptr, None, b.ptr, 512, N, K))
     return OpsWorkload(env, ops, burst=10)
 
 
