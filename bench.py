@@ -17,7 +17,8 @@ Also reported in the same JSON line:
   gemm_set_graph_replay  the same step captured once as a hipGraph and replayed (no faster: the
                 gap between dependent launches is the same inside a graph)
   gemv_int8     INT8 decode GEMV GB/s per trunk shape, cold (rotating > 512 MB of weight copies,
-                so every launch streams from HBM) and warm (same weights every launch), the
+                so every launch streams from HBM) and warm (same weights every launch), beside the
+                same shape with fp16 weights in alternating rounds (medians, [min, max], verdict), the
                 48-GEMV trunk chain of one decode step, and the same kernel on the INT8 tied head
                 (38.6 MB per launch, where the launch floor no longer hides the streaming rate)
   head_gemv     fp16 tied-head GEMV (77.3 MB) cold / warm
@@ -342,52 +343,69 @@ def copies_for(nbytes, floor=600e6):
 
 
 def bench_gemv(B, quick=False):
-    """quick: a few launches per leg (the counter runs profile every dispatch)."""
+    """quick: a few launches per leg (the counter runs profile every dispatch).
+
+    Per trunk shape, INT8 (gpt2_gemv_int8) against fp16 weights (gpt2_gemv_fp16), cold and warm, in
+    alternating rounds (INT8 first on even rounds) so that a change of the box's state during the leg
+    lands on both sides alike: a cold sample is one pass over the rotating copies (us per launch), a
+    warm one the mean of a burst of launches on one copy; median and [min, max] per side, and the
+    overlap verdict of bench/ab.py."""
+    ab = importlib.import_module("ab")
     rng = np.random.default_rng(4321)
-    n_cold, n_warm, n_chain, n_head = (1, 20, 2, 10) if quick else (5, 2000, 200, 200)
+    rounds, n_cold, n_warm, n_chain, n_head = (1, 1, 20, 2, 10) if quick else (7, 5, 300, 200, 200)
     L = B.L
     res = {}
     x768 = B.dev(f16(rng, 768, 1.0))
     x3072 = B.dev(f16(rng, 3072, 1.0))
     y = B.empty(VOCAB * 2)
     chain = []
+
     for name, N, K in TRUNK_GEMV:
         x = x3072 if K == 3072 else x768
         w16 = B.dev(f16(rng, (N, K), 0.02))
         q, s = quantize_dev(B, w16, N, K)
         b = B.dev(f16(rng, N, 0.01))
         algo = N * K + 4 * N + 2 * K + 2 * N + 2 * N
-        R = copies_for(N * K)
-        big = B.empty(R * N * K)
+        algo16 = 2 * N * K + 2 * K + 2 * N + 2 * N
+        R, R16 = copies_for(N * K), copies_for(2 * N * K)
+        big, big16 = B.empty(R * N * K), B.empty(R16 * N * K * 2)
         for r in range(R):
             L.gpt2_d2d(big.at(r * N * K), q.ptr, N * K)
-        L.gpt2_sync()
-        cold_ops = [B.op(3, y.ptr, x.ptr, big.at(r * N * K), s.ptr, b.ptr, 1, N, K) for r in range(R)]
-        ms_cold, _ = B.run_ops(cold_ops, 1, n_cold)
-        ms_cold /= R
-        ms_warm, _ = B.run_ops([B.op(3, y.ptr, x.ptr, q.ptr, s.ptr, b.ptr, 1, N, K)], 5 if quick else 50, n_warm)
-        res[name] = {"N": N, "K": K, "bytes": algo, "copies": R,
-                     "cold_us": round(ms_cold * 1e3, 3), "cold_GBs": round(algo / (ms_cold * 1e-3) / 1e9, 1),
-                     "warm_us": round(ms_warm * 1e3, 3), "warm_GBs": round(algo / (ms_warm * 1e-3) / 1e9, 1)}
-        big.free()
-        # the same shape with fp16 weights (gpt2_gemv_fp16): twice the weight bytes
-        algo16 = 2 * N * K + 2 * K + 2 * N + 2 * N
-        R16 = copies_for(2 * N * K)
-        big = B.empty(R16 * N * K * 2)
         for r in range(R16):
-            L.gpt2_d2d(big.at(r * N * K * 2), w16.ptr, N * K * 2)
+            L.gpt2_d2d(big16.at(r * N * K * 2), w16.ptr, N * K * 2)
         L.gpt2_sync()
-        ms16c, _ = B.run_ops([B.op(2, y.ptr, x.ptr, big.at(r * N * K * 2), None, b.ptr, 1, N, K) for r in range(R16)],
-                             1, n_cold)
-        ms16c /= R16
-        ms16w, _ = B.run_ops([B.op(2, y.ptr, x.ptr, w16.ptr, None, b.ptr, 1, N, K)], 5 if quick else 50, n_warm)
+        cold = {8: [B.op(3, y.ptr, x.ptr, big.at(r * N * K), s.ptr, b.ptr, 1, N, K) for r in range(R)],
+                16: [B.op(2, y.ptr, x.ptr, big16.at(r * N * K * 2), None, b.ptr, 1, N, K) for r in range(R16)]}
+        warm = {8: [B.op(3, y.ptr, x.ptr, q.ptr, s.ptr, b.ptr, 1, N, K)], 16: [B.op(2, y.ptr, x.ptr, w16.ptr, None, b.ptr, 1, N, K)]}
+        for d in (8, 16):
+            B.run_ops(cold[d], 0, 1)
+            B.run_ops(warm[d], 5, 5)
+        sc, sw = {8: [], 16: []}, {8: [], 16: []}
+        for rnd in range(rounds):
+            for d in ((8, 16) if rnd % 2 == 0 else (16, 8)):
+                ms, _ = B.run_ops(cold[d], 0, 1)
+                sc[d].append(ms * 1e3 / len(cold[d]))
+                ms, _ = B.run_ops(warm[d], 0, n_warm)
+                sw[d].append(ms * 1e3)
         big.free()
-        res[name]["fp16"] = {"bytes": algo16, "copies": R16, "cold_us": round(ms16c * 1e3, 3),
-                             "cold_GBs": round(algo16 / (ms16c * 1e-3) / 1e9, 1), "warm_us": round(ms16w * 1e3, 3),
-                             "warm_GBs": round(algo16 / (ms16w * 1e-3) / 1e9, 1)}
-        res[name]["int8_speedup_cold"] = round(ms16c / ms_cold, 3)
-        res[name]["int8_speedup_warm"] = round(ms16w / ms_warm, 3)
+        big16.free()
+        c8, c16, w8, w16s = ab.stats(sc[8]), ab.stats(sc[16]), ab.stats(sw[8]), ab.stats(sw[16])
+        res[name] = {"N": N, "K": K, "bytes": algo, "copies": R,
+                     "cold_us": round(c8["median"], 3), "cold_us_min_max": [round(c8["min"], 3), round(c8["max"], 3)],
+                     "cold_GBs": round(algo / (c8["median"] * 1e-6) / 1e9, 1),
+                     "warm_us": round(w8["median"], 3), "warm_GBs": round(algo / (w8["median"] * 1e-6) / 1e9, 1)}
+        res[name]["fp16"] = {"bytes": algo16, "copies": R16, "cold_us": round(c16["median"], 3),
+                             "cold_us_min_max": [round(c16["min"], 3), round(c16["max"], 3)],
+                             "cold_GBs": round(algo16 / (c16["median"] * 1e-6) / 1e9, 1),
+                             "warm_us": round(w16s["median"], 3),
+                             "warm_GBs": round(algo16 / (w16s["median"] * 1e-6) / 1e9, 1)}
+        v = ab.verdict(c16, c8)
+        res[name]["int8_speedup_cold"] = v["speedup_b_vs_a"]
+        res[name]["cold_verdict"] = v["verdict"] if rounds >= 3 else "one round (quick run): no verdict"
+        res[name]["int8_speedup_warm"] = ab.verdict(w16s, w8)["speedup_b_vs_a"]
         log(f"gemv {name}: {res[name]}")
+    res["per_shape_method"] = (f"{rounds} alternating rounds per shape, INT8 first on even rounds; cold sample = one pass "
+                               f"over the rotating copies, warm sample = mean of {n_warm} launches; medians")
     # the 48 INT8 GEMVs of one decode step, distinct weights per layer, back to back
     chain_bytes = 0
     for layer in range(N_LAYER):
