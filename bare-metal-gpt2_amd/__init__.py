@@ -181,6 +181,9 @@ SIGNATURES = {
     "gpt2_tune_gemm_ln_count": (_i, []),
     "gpt2_tune_gemm_ln_name": (C.c_char_p, [_i]),
     "gpt2_tune_gemm_ln_force": (None, [_i]),
+    "gpt2_tune_gemm_skinny": (None, [_i]),
+    "gpt2_tune_gemm_skinny_max": (_i, [_i]),
+    "gpt2_tune_gemm_skinny_calls": (_i, []),
     "gpt2_tune_gemm_ln": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i]),
     "gpt2_tune_gemv_count": (_i, []),
     "gpt2_tune_gemv_name": (C.c_char_p, [_i]),

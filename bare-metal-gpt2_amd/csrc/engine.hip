@@ -30,6 +30,9 @@ void attn_decode_append(uint16_t *att, const uint16_t *qkv, uint16_t *K, uint16_
 bool gemv_fused(uint16_t *C, const uint16_t *x, const void *W, const float *Ws, const uint16_t *bias, int N, int K,
                 bool qw, const uint16_t *ln_g, const uint16_t *ln_b, int epi, const uint16_t *resid);
 int gemm_ln_forced();
+bool gemm_skinny(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const uint16_t *bias, int M, int N,
+                 int K, bool qw, int epi, const uint16_t *resid, const uint16_t *ln_g, const uint16_t *ln_b);
+int skinny_max_m(bool qw);
 bool gemm_lnfold(int epi, uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const uint16_t *bias, int M,
                  int N, int K, bool qw, const uint16_t *resid, const LnFold &lf);
 void embed_lnf(uint16_t *x, uint16_t *xg, float2 *stats, const uint16_t *wte, const uint16_t *wpe, const int *ids,
@@ -258,16 +261,19 @@ static void matmul_site(const GPT2Backend *be, bool fused, gpt2_half *C, const g
     }
 }
 
-// LayerNorm(X) followed by a matmul site (QKV: no epilogue; fc: gelu): one LayerNorm-panel GEMM
-// launch when a panel config is forced (gpt2_tune_gemm_ln_force; off by default, slower than the two
-// launches) and the fused prefill may use it (ln_fuse also requires this library's LayerNorm, whose
-// arithmetic the panel repeats bit for bit), else the backend's LayerNorm into lnbuf, then the site.
+// LayerNorm(X) followed by a matmul site (QKV: no epilogue; fc: gelu), when the fused prefill may
+// fuse them (ln_fuse also requires this library's LayerNorm, whose arithmetic both fused forms repeat
+// bit for bit): one LayerNorm-panel GEMM launch when a panel config is forced
+// (gpt2_tune_gemm_ln_force; off by default, slower than the two launches); else, for a few rows, the
+// skinny GEMM with its LayerNorm prologue; else the backend's LayerNorm into lnbuf, then the site.
 static void ln_matmul_site(const GPT2Backend *be, bool fused, bool ln_fuse, gpt2_half *C, const gpt2_half *X,
                            const gpt2_half *ln_g, const gpt2_half *ln_b, gpt2_half *lnbuf, const gpt2_half *Wh,
                            const GPT2QW *Wq, const gpt2_half *bias, int M, int N, int K, int epi) {
     const bool q = be->matmul_q && Wq && Wq->q;
-    if (ln_fuse && gemm_ln(C, X, ln_g, ln_b, q ? (const void *)Wq->q : (const void *)Wh, q ? Wq->s : nullptr, bias, M,
-                           N, K, q, epi, -1))
+    const void *W = q ? (const void *)Wq->q : (const void *)Wh;
+    if (ln_fuse && gemm_ln(C, X, ln_g, ln_b, W, q ? Wq->s : nullptr, bias, M, N, K, q, epi, -1)) return;
+    if (ln_fuse && gemm_ln_forced() < 0 &&
+        gemm_skinny(C, X, W, q ? Wq->s : nullptr, bias, M, N, K, q, epi, nullptr, ln_g, ln_b))
         return;
     be->layernorm(lnbuf, X, ln_g, ln_b, M, K);
     if (epi == EPI_NONE) gpt2_matmul_dispatch(be, C, lnbuf, Wh, Wq, bias, M, N, K);
@@ -303,6 +309,7 @@ extern "C" int gpt2_tune_prefill_lnfold_sites(void) { return g_lnfold_sites; }
 
 static bool lnfold_wanted(int T, bool int8) {
     if (g_lnfold >= 0) return g_lnfold == 1;
+    if (T <= skinny_max_m(int8)) return false;   // the skinny GEMM's LayerNorm prologue takes these
     return T <= (int8 ? 256 : 128);
 }
 

@@ -1121,6 +1121,9 @@ static int pick_cfg(int M, int N, int K, bool qw = false) {
     return last;
 }
 
+bool gemm_skinny(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const uint16_t *bias, int M, int N,
+                 int K, bool qw, int epi, const uint16_t *resid, const uint16_t *ln_g, const uint16_t *ln_b);
+
 static bool mfma_ok(const void *A, const void *W, int K, bool qw) {
     if (qw) return (K % 16) == 0 && aligned16(A) && aligned16(W);
     return (K % 8) == 0 && aligned16(A) && aligned16(W);
@@ -1171,6 +1174,10 @@ void gemm(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, const 
         gemv(C, A, W, Ws, bias, N, K, qw, -1);
         return;
     }
+    // A few rows of A (short prompts): the product is a weight stream, taken by the skinny kernel
+    // (gemm_skinny.hip) where its shapes allow.  Tuning runs that force a tile config keep the tiles.
+    if (cfg < 0 && forced_cfg() < 0 && gemm_skinny(C, A, W, Ws, bias, M, N, K, qw, EPI_NONE, nullptr, nullptr, nullptr))
+        return;
     // K == 0 (an empty sum, C = bias or 0) falls through to the generic kernel.
     if (K > 0 && mfma_ok(A, W, K, qw)) {
         const int c = (cfg >= 0 && cfg < kNumCfgs && cfg_usable(cfg, M, N, K)) ? cfg : pick_cfg(M, N, K, qw);
@@ -1196,6 +1203,7 @@ bool gemm_fused(uint16_t *C, const uint16_t *A, const void *W, const float *Ws, 
     // the residual form reads the residual 4 columns (8 bytes) at a time
     if (epi == EPI_RESID && (!resid || N % 4 || (((uintptr_t)resid | (uintptr_t)C) & 7u))) return false;
     if (epi != EPI_GELU && epi != EPI_RESID) return false;
+    if (forced_cfg() < 0 && gemm_skinny(C, A, W, Ws, bias, M, N, K, qw, epi, resid, nullptr, nullptr)) return true;
     const int c = pick_cfg(M, N, K, qw);
     if (c < 0) return false;
     const GemmFn fn = kCfgs[c].fused[qw ? 1 : 0][epi == EPI_RESID ? 1 : 0];

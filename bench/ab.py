@@ -30,6 +30,8 @@ SPEC: comma-separated key=value knobs; an empty SPEC ("") is the library's defau
   much device memory before the workload's own buffers, as bench.py's measured peaks leg does)
   epi=gelu|resid  gemm_shape / gemm_set: the fused-epilogue GEMM the prefill runs (gelu after the
                  product, or the residual added in place) instead of the plain one
+  m=M            gemm_shape / gemm_set: rows of A (default 512)
+  skinny=N       the skinny GEMM takes M up to N (gpt2_tune_gemm_skinny; 0: never, -1: the default)
 
 Examples:
   python bench/ab.py gemm_set --a "" --b gemm_cfg=12
@@ -129,6 +131,16 @@ def big_alloc(env, gib):
     d.free()
 
 
+def skinny_knob(env, knobs):
+    """Applies the skinny knob for one sample (-1: the library's default); returns -1, the value to
+    restore, or None when the build has no such hook."""
+    L = env.L
+    if not hasattr(L, "gpt2_tune_gemm_skinny"):
+        return None
+    L.gpt2_tune_gemm_skinny(int(knobs.get("skinny", -1)))
+    return -1
+
+
 class OpsWorkload:
     """A list of harness ops timed as one step; a sample is the mean step time over `burst` steps."""
 
@@ -142,10 +154,13 @@ class OpsWorkload:
         cfg = int(knobs.get("gemm_cfg", -1))
         if hasattr(env.L, "gpt2_tune_gemm_force"):
             env.L.gpt2_tune_gemm_force(cfg)
+        prev = skinny_knob(env, knobs)
         ms = C.c_float()
         rc = env.H.gpt2_bench_ops(self.arr, self.n, 2, self.burst, C.byref(ms), None)
         if hasattr(env.L, "gpt2_tune_gemm_force"):
             env.L.gpt2_tune_gemm_force(-1)
+        if prev is not None:
+            env.L.gpt2_tune_gemm_skinny(prev)
         if rc:
             env.pkg.check("gpt2_bench_ops")
             raise RuntimeError(f"gpt2_bench_ops rc={rc}")
@@ -155,15 +170,16 @@ class OpsWorkload:
 def make_gemm_set(env, knobs, int8=False, only=None):
     rng = np.random.default_rng(1234)
     H = env.harness
-    X = env.dev(f16(rng, (512, 768), 1.0))
-    Xf = env.dev(f16(rng, (512, 3072), 1.0))
+    M = int(knobs.get("m", 512))
+    X = env.dev(f16(rng, (M, 768), 1.0))
+    Xf = env.dev(f16(rng, (M, 3072), 1.0))
     # plain GEMM (harness kind 0 fp16 / 1 INT8), or the fused epilogue: 8 gelu, 6 residual added into C
     # (C then starts as data, not as whatever the allocation held)
     epi = {"gelu": 8, "resid": 6}.get(knobs.get("epi", ""), None)
     if epi is None:
-        outs = {k: env.empty(512 * SHAPES[k][0] * 2) for k in ORDER}
+        outs = {k: env.empty(M * SHAPES[k][0] * 2) for k in ORDER}
     else:
-        outs = {k: env.dev(f16(np.random.default_rng(99), (512, SHAPES[k][0]), 1.0)) for k in ORDER}
+        outs = {k: env.dev(f16(np.random.default_rng(99), (M, SHAPES[k][0]), 1.0)) for k in ORDER}
     ops = []
     for _ in range(12):
         for k in ORDER if only is None else [only]:
@@ -173,10 +189,10 @@ def make_gemm_set(env, knobs, int8=False, only=None):
             if int8:
                 W = env.dev(rng.integers(-127, 128, (N, K), dtype=np.int8))
                 s = env.dev((rng.random(N, dtype=np.float32) * np.float32(2e-4) + np.float32(1e-4)))
-                ops.append(H.GPT2BenchOp(epi or 1, outs[k].ptr, A.ptr, W.ptr, s.ptr, b.ptr, 512, N, K))
+                ops.append(H.GPT2BenchOp(epi or 1, outs[k].ptr, A.ptr, W.ptr, s.ptr, b.ptr, M, N, K))
             else:
                 W = env.dev(f16(rng, (N, K), 0.02))
-                ops.append(H.GPT2BenchOp(epi or 0, outs[k].ptr, A.ptr, W.ptr, None, b.ptr, 512, N, K))
+                ops.append(H.GPT2BenchOp(epi or 0, outs[k].ptr, A.ptr, W.ptr, None, b.ptr, M, N, K))
     return OpsWorkload(env, ops, burst=10)
 
 
@@ -334,6 +350,7 @@ class PrefillWorkload:
             L.gpt2_tune_prefill_persistent(int(knobs.get("prefill_persistent", -1)))
         if hasattr(L, "gpt2_tune_prefill_lnfold"):
             L.gpt2_tune_prefill_lnfold(int(knobs.get("lnfold", -1)))
+        prev = skinny_knob(env, knobs)
         be = env.pkg.backend(backend)
         out = []
         for _ in range(5):
@@ -346,6 +363,8 @@ class PrefillWorkload:
             L.gpt2_tune_prefill_persistent(-1)
         if hasattr(L, "gpt2_tune_prefill_lnfold"):
             L.gpt2_tune_prefill_lnfold(-1)
+        if prev is not None:
+            L.gpt2_tune_gemm_skinny(prev)
         env.pkg.check("prefill")
         return float(np.median(out[1:]))
 
@@ -353,7 +372,7 @@ class PrefillWorkload:
 def make_workload(env, name, knobs):
     big_alloc(env, float(knobs.get("big_alloc", 0)))
     if name == "gemm_set":
-        return make_gemm_set(env, knobs)
+        return make_gemm_set(env, knobs, int8=knobs.get("dtype") == "int8")
     if name == "gemm_int8_set":
         return make_gemm_set(env, knobs, int8=True)
     if name == "gemm_shape":
@@ -419,7 +438,7 @@ def main():
         env = Env()
         wa = make_workload(env, args.workload, ka)
         # the same workload object serves both sides unless their buffers would differ
-        same = all(ka.get(k) == kb.get(k) for k in ("big_alloc", "dtype", "shape", "gemv_cfg", "cold"))
+        same = all(ka.get(k) == kb.get(k) for k in ("big_alloc", "dtype", "shape", "gemv_cfg", "cold", "epi", "m"))
         wb = wa if same else make_workload(env, args.workload, kb)
         wa.sample(ka)
         wb.sample(kb)

@@ -145,10 +145,13 @@ def test_lnfold_vs_oracle(pkg, L, synth, model, backend, T):
     assert kl_rows(ref["logits"], lg).max() < 0.02
 
 
-@pytest.mark.parametrize("backend,T,sites", [("flash", 128, SITES), ("flash", 129, 0), ("int8", 256, SITES),
+@pytest.mark.parametrize("backend,T,sites", [("flash", 16, 0), ("flash", 32, 0), ("flash", 33, SITES), ("int8", 64, 0),
+                                              ("int8", 65, SITES),
+                                              ("flash", 128, SITES), ("flash", 129, 0), ("int8", 256, SITES),
                                               ("int8", 257, 0), ("flash", 512, 0)])
 def test_lnfold_default_by_length(pkg, L, synth, model, backend, T, sites):
-    """Left at its default, the fold runs where it measured faster: T <= 128, INT8 up to 256."""
+    """Left at its default, the fold runs where it measured faster: T <= 128, INT8 up to 256, above the
+    skinny GEMM's rows (T <= 32 fp16, <= 64 INT8: its LayerNorm prologue takes LN1 and LN2)."""
     ids = synth.token_ids(T, seed=T)
     if backend == "int8":
         model.quantize()
@@ -210,7 +213,7 @@ def hip_runtime():
 
 @pytest.mark.parametrize("warm", [True, False])
 def test_lnfold_under_graph_capture(pkg, L, synth, warm):
-    """gpt2_forward_cuda at T = 64 (inside the fold's default range) captured into a HIP graph on a
+    """gpt2_forward_cuda at T = 96 (inside the fold's default range) captured into a HIP graph on a
     stream of its own.  warm: the weights' fold constants exist (an eager call built them), so the
     captured forward runs folded (47 sites) and every replay equals the eager folded call bit for bit.
     cold: fresh weights, so the constants would need an allocation, which is not made under capture;
@@ -219,7 +222,7 @@ def test_lnfold_under_graph_capture(pkg, L, synth, warm):
     builds the constants; the instantiated graph is unaffected)."""
     hip = hip_runtime()
     m = pkg.Model(synth.make_body(seed=21 if warm else 22, plain=False))
-    T = 64
+    T = 96
     ids, other = synth.token_ids(T, seed=61), synth.token_ids(T, seed=62)
     d_ids, d_other = pkg.Dev.from_numpy(np.asarray(ids, np.int32)), pkg.Dev.from_numpy(np.asarray(other, np.int32))
     scr = pkg.Scratch(T)

@@ -118,14 +118,17 @@ def test_prefill_forward_backends_agree(pkg, L, synth, model):
 
 
 @pytest.mark.parametrize("backend,T,ln", [("flash", 200, -1), ("int8", 200, -1), ("tiled", 33, -1), ("int8", 512, -1),
-                                          ("flash", 200, 1), ("int8", 512, 2)])
+                                          ("flash", 200, 1), ("int8", 512, 2), ("flash", 16, -1), ("int8", 40, -1),
+                                          ("int8", 2, -1), ("flash", 32, -1), ("int8", 64, -1)])
 def test_fused_prefill_bit_identical(pkg, L, synth, model, backend, T, ln):
     """The fused launch sequence of the prefill (gelu and the residual adds in GEMM epilogues, the K/V
     cache fill inside the attention launch; the persistent trunk kernel and the LayerNorm fold
     switched off) equals the unfused reference sequence bit for bit: every layer's residual stream,
     the final LayerNorm, all logits rows and the whole K/V cache.  ln >= 0 also runs LN1 -> QKV and
     LN2 -> fc as LayerNorm-panel GEMMs with that config (at T where the plain GEMMs have one k group).
-    The fold moves rounding points; test_gpu_lnfold holds it to the fp16 gates."""
+    At T <= 32 (fp16) or 64 (INT8) the fused sequence runs LN1 -> QKV and LN2 -> fc as the skinny
+    GEMM with its LayerNorm prologue (and the other GEMMs as skinny fused epilogues), the unfused one
+    the LayerNorm launch and the plain skinny GEMM.  The fold moves rounding points; test_gpu_lnfold holds it to the fp16 gates."""
     ids = synth.token_ids(T, seed=T + 7)
     d_ids = pkg.Dev.from_numpy(np.asarray(ids, np.int32))
     if backend == "int8":
@@ -142,10 +145,14 @@ def test_fused_prefill_bit_identical(pkg, L, synth, model, backend, T, ln):
             caps = pkg.GPT2CapsGPU()
             caps.logits, caps.logits_all, caps.final_ln, caps.blocks = logits.ptr, 1, fin.ptr, blocks.ptr
             L.gpt2_memset(kv.kv.data, 0, kv.kv.bytes)
+            calls = L.gpt2_tune_gemm_skinny_calls()
             L.gpt2_prefill_fill_cache(pkg.backend(backend), C.byref(model.gpu), C.byref(kv.kv), d_ids.ptr, T,
                                       C.byref(scr.s), C.byref(caps))
             L.gpt2_sync()
             pkg.check("prefill fused=%d" % fused)
+            # the 48 trunk GEMMs of a short prompt run as the skinny kernel in both sequences
+            skinny = 48 if 2 <= T <= L.gpt2_tune_gemm_skinny_max(backend == "int8") else 0
+            assert L.gpt2_tune_gemm_skinny_calls() - calls == skinny, (fused, T)
             assert kv.kv.len == T
             cache = np.empty(kv.kv.bytes // 2, np.uint16)
             assert L.gpt2_d2h(cache.ctypes.data, kv.kv.data, cache.nbytes) == 0
