@@ -24,7 +24,8 @@ Also reported in the same JSON line:
   head_gemv     fp16 tied-head GEMV (77.3 MB) cold / warm
   gemm_int8_set the same P=512 trunk set with INT8 weights (the config-5 prefill GEMMs)
   head_gemm     the tied head as a prefill GEMM, [512x768] . [768x50257]^T (39.5 GFLOP)
-  gemm_m_sweep  the four trunk GEMMs at M in {1, 64, 128, 256, 512, 1024}, fp16 and INT8 weights
+  gemm_m_sweep  the four trunk GEMMs at M in {1, 16, 32, 64, 128, 256, 512, 1024}, fp16 and INT8
+                weights, with the kernel each M takes (GEMV at M = 1, the skinny GEMM for short prompts)
   measured_peaks  this box's HBM read stream and fp16 MFMA issue rate, beside the datasheet peaks
   bandwidth_guard  every cold (HBM) GB/s leg against the measured read stream (the reference's bug
                 line): legs above it are listed as suspicious
@@ -534,10 +535,11 @@ def bench_gemm_extra(B, steps):
 
 
 # ------------------------------------------------------------------------------ M sweep
-def bench_m_sweep(B, Ms=(1, 64, 128, 256, 512, 1024), iters=30):
+def bench_m_sweep(B, Ms=(1, 16, 32, 64, 128, 256, 512, 1024), iters=30):
     """The four trunk GEMMs across prompt lengths (the reference's bench/profile_matmul.cu:6-16 sweep):
     per shape, 12 layers' distinct weights back to back through gpt2_matmul_tiled / gpt2_matmul_int8,
-    per-launch microseconds and TFLOP/s (M = 1 runs the GEMV path, as the launchers route it)."""
+    per-launch microseconds and TFLOP/s (M = 1 runs the GEMV path and short prompts the skinny GEMM,
+    as the launchers route them)."""
     rng = np.random.default_rng(555)
     L = B.L
     out = {}
@@ -559,9 +561,10 @@ def bench_m_sweep(B, Ms=(1, 64, 128, 256, 512, 1024), iters=30):
                 ms, _ = B.run_ops(ops, 3, iters)
                 us = ms * 1e3 / N_LAYER
                 cfg = L.gpt2_tune_gemm_pick_q(M, N, K, 1 if kind == "int8" else 0)
+                skinny = hasattr(L, "gpt2_tune_gemm_skinny_max") and 2 <= M <= L.gpt2_tune_gemm_skinny_max(kind == "int8")
                 rows.append({"gemm": name, "M": M, "us": round(us, 3),
                              "tflops": round(2.0 * M * N * K / (us * 1e-6) / 1e12, 2),
-                             "kernel": "gemv" if M == 1 else L.gpt2_tune_gemm_name(cfg).decode()})
+                             "kernel": "gemv" if M == 1 else "skinny" if skinny else L.gpt2_tune_gemm_name(cfg).decode()})
             B.keep.clear()
         out[kind] = rows
     return out
@@ -629,8 +632,9 @@ def bench_forward_t64(B, reps=20):
 def bench_prefill(B, reps=30):
     """The whole prefill (gpt2_prefill_fill_cache: embedding, 12 layers with attention and the K/V
     fill, final LayerNorm, last-row logits) at P=512 with fp16 and with INT8 trunk weights, and at
-    P=128 with the LayerNorm fold at its default (on there) and off; one hipEvent pair per forward
-    on the library's stream, median and [min, max] of `reps` forwards after 3 untimed ones.
+    P=128 with the LayerNorm fold at its default (on there) and off, and at P=16 with the skinny GEMM
+    at its default (on there) and off; one hipEvent pair per forward on the library's stream, median
+    and [min, max] of `reps` forwards after 3 untimed ones.
     prefill_trunk_gemm_tflops = the 48 trunk GEMMs' 86.97 GFLOP / the fp16 P=512 forward: attention,
     LayerNorms and the head row sit in the denominator, so it is a lower bound on the trunk rate."""
     pkg, L = B.pkg, B.L
@@ -640,7 +644,7 @@ def bench_prefill(B, reps=30):
         getattr(hip, fn).restype = C.c_int
     stream = C.c_void_p(L.gpt2_get_stream())
 
-    def run(model, backend, T, lnfold=-1):
+    def run(model, backend, T, lnfold=-1, skinny=-1):
         kv, scr = pkg.KVCache(T), pkg.Scratch(T)
         d_ids = B.dev(synth.token_ids(T, seed=1234))
         logits = B.empty(VOCAB * 2)
@@ -648,6 +652,7 @@ def bench_prefill(B, reps=30):
         caps.logits, caps.logits_all = logits.ptr, 0
         be = pkg.backend(backend)
         L.gpt2_tune_prefill_lnfold(lnfold)
+        L.gpt2_tune_gemm_skinny(skinny)
         ev = [(C.c_void_p(), C.c_void_p()) for _ in range(reps)]
         for a, b in ev:
             hip.hipEventCreate(C.byref(a))
@@ -670,6 +675,7 @@ def bench_prefill(B, reps=30):
                 ms.append(t.value)
         finally:
             L.gpt2_tune_prefill_lnfold(-1)
+            L.gpt2_tune_gemm_skinny(-1)
             for a, b in ev:
                 hip.hipEventDestroy(a)
                 hip.hipEventDestroy(b)
@@ -679,16 +685,20 @@ def bench_prefill(B, reps=30):
 
     model = pkg.Model(seeded_body())
     out = {"fp16_p512": run(model, "flash", 512), "fp16_p128": run(model, "flash", 128),
-           "fp16_p128_lnfold_off": run(model, "flash", 128, 0)}
+           "fp16_p128_lnfold_off": run(model, "flash", 128, 0), "fp16_p16": run(model, "flash", 16),
+           "fp16_p16_skinny_off": run(model, "flash", 16, skinny=0)}
     model.quantize()
     out["int8_p512"] = run(model, "int8", 512)
     out["int8_p128"] = run(model, "int8", 128)
     out["int8_p128_lnfold_off"] = run(model, "int8", 128, 0)
+    out["int8_p16"] = run(model, "int8", 16)
+    out["int8_p16_skinny_off"] = run(model, "int8", 16, skinny=0)
     model.free()
     trunk_flop = N_LAYER * sum(2.0 * M_PREFILL * N * K for _, N, K in GEMM_SET)
     out["prefill_trunk_gemm_tflops"] = round(trunk_flop / (out["fp16_p512"]["ms_median"] * 1e-3) / 1e12, 2)
     for w in ("fp16", "int8"):
         out[f"{w}_p128_lnfold_speedup"] = round(out[f"{w}_p128_lnfold_off"]["ms_median"] / out[f"{w}_p128"]["ms_median"], 3)
+        out[f"{w}_p16_skinny_speedup"] = round(out[f"{w}_p16_skinny_off"]["ms_median"] / out[f"{w}_p16"]["ms_median"], 3)
     return out
 
 
