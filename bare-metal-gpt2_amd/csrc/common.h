@@ -141,6 +141,60 @@ __device__ __forceinline__ void ln_row768(const f16x4 (&x)[3], const f16x4 (&g)[
         }
 }
 
+// ln_row768 on R rows at once (row r in x[r], lane layout as above): each row goes through exactly
+// ln_row768's operations, so the bits are those of R calls, but the rows' cross-lane sums are
+// issued together, so their latencies (each wave_sum ends in two LDS permutes) overlap instead of
+// running one row after another.
+template <int R>
+__device__ __forceinline__ void ln_rows768(const f16x4 (&x)[R][3], const f16x4 (&g)[3], const f16x4 (&b)[3],
+                                           f16x4 (&o)[R][3]) {
+    float v[R][12], s[R], q[R], mean[R], rstd[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[r][4 * i + c] = (float)x[r][i][c];
+        s[r] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 12; ++i) s[r] += v[r][i];
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) s[r] = row16_sum(s[r]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) s[r] += __shfl_xor(s[r], 16, 64);
+#pragma unroll
+    for (int r = 0; r < R; ++r) s[r] += __shfl_xor(s[r], 32, 64);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        mean[r] = s[r] / (float)GPT2_N_EMBD;
+        q[r] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 12; ++i) {
+            const float d = v[r][i] - mean[r];
+            q[r] = __builtin_fmaf(d, d, q[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) q[r] = row16_sum(q[r]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) q[r] += __shfl_xor(q[r], 16, 64);
+#pragma unroll
+    for (int r = 0; r < R; ++r) q[r] += __shfl_xor(q[r], 32, 64);
+#pragma unroll
+    for (int r = 0; r < R; ++r) rstd[r] = 1.0f / sqrtf(q[r] / (float)GPT2_N_EMBD + GPT2_LN_EPS);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                float y = __builtin_fmaf((v[r][4 * i + c] - mean[r]) * rstd[r], (float)g[i][c], (float)b[i][c]);
+                asm volatile("" : "+v"(y));
+                o[r][i][c] = (f16)y;
+            }
+}
+
 // gelu_new, the tanh form (model/config.h:41-42): 0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))).
 // The decode kernels (fused GEMV epilogue, persistent step) use this form.
 __device__ __forceinline__ float gelu_tanh(float v) {

@@ -59,18 +59,38 @@ __global__ __launch_bounds__(64 * SKN_W) void k_gemm_skinny(uint16_t *__restrict
     const int n0 = nb * 16, m0 = mb * SKN_MB;
     const int kw0 = wave * KW;
 
-    // This lane's share of W row n0 + lrow (N % 16 == 0, so the row exists): every load issued now.
-    uint4 wl[NL];
+    // Loads, in this order (loads complete in issue order, so a wait for one is a wait for every
+    // load issued before it): the LayerNorm prologue's rows and gamma / beta (L2-resident, needed
+    // first), this lane's share of W row n0 + lrow (N % 16 == 0: the row exists; all of it in flight
+    // at once, from HBM the longest wait), then the epilogue operands.  Compiler barriers keep the
+    // order (left to itself the compiler moves the weight loads behind the LayerNorm and the epilogue
+    // operands behind the A block's wait).
+    f16x4 lg[3], lb[3], lx[4][3];   // LayerNorm prologue: rows wave + 4 r; lane l: elements 256 i + 4 l ..
+    if constexpr (LNP) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint16_t *xr = A + (size_t)min(m0 + wave + 4 * r, M - 1) * K;
+#pragma unroll
+            for (int i = 0; i < 3; ++i) lx[r][i] = *reinterpret_cast<const f16x4 *>(xr + 256 * i + 4 * lane);
+        }
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            lg[i] = *reinterpret_cast<const f16x4 *>(ln_g + 256 * i + 4 * lane);
+            lb[i] = *reinterpret_cast<const f16x4 *>(ln_b + 256 * i + 4 * lane);
+        }
+        asm volatile("" ::: "memory");
+    }
+    i32x4 wl[NL];
     {
         const char *wrow = reinterpret_cast<const char *>(Wv) + (size_t)(n0 + lrow) * K * (QW ? 1 : 2);
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
             const int k = kw0 + (QW ? skn_k<true>(2 * i, g) : skn_k<false>(i, g));
-            wl[i] = *reinterpret_cast<const uint4 *>(wrow + (size_t)k * (QW ? 1 : 2));
+            wl[i] = *reinterpret_cast<const i32x4 *>(wrow + (size_t)k * (QW ? 1 : 2));
         }
     }
-    // Epilogue operands of the lane's outputs C[m][nbase .. nbase+3], loaded with the weights (rows
-    // past M read row M-1 and store nothing); the residual may alias C: this lane alone writes them.
+    // the lane's outputs C[m][nbase .. nbase+3]: scales, bias and residual (rows past M read row M-1
+    // and store nothing; the residual may alias C: this lane alone writes those elements)
     const int nbase = n0 + 4 * g, m = m0 + lrow;
     float sc[4];
     uint32_t bs[4];
@@ -82,31 +102,27 @@ __global__ __launch_bounds__(64 * SKN_W) void k_gemm_skinny(uint16_t *__restrict
     }
     uint2 rs = {0u, 0u};
     if constexpr (EPI == EPI_RESID) rs = *reinterpret_cast<const uint2 *>(resid + (size_t)min(m, M - 1) * N + nbase);
+    asm volatile("" ::: "memory");
+    if constexpr (LNP) {
+        // the LayerNorm's inputs pass through here, so none of its arithmetic is scheduled ahead of
+        // the loads above (the compiler would otherwise issue the weight loads after it)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int i = 0; i < 3; ++i) asm volatile("" : "+v"(lx[r][i]) : : "memory");
+    }
 
     if constexpr (LNP) {
-        // rows wave + 4 r of the block: lane l holds elements 256 i + 4 l .. +3, normalized as the
-        // LayerNorm kernel does, written where the direct-to-LDS load would have put them
-        f16x4 lg[3], lb[3], lx[4][3];
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            lg[i] = *reinterpret_cast<const f16x4 *>(ln_g + 256 * i + 4 * lane);
-            lb[i] = *reinterpret_cast<const f16x4 *>(ln_b + 256 * i + 4 * lane);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint16_t *xr = A + (size_t)min(m0 + wave + 4 * r, M - 1) * K;
-#pragma unroll
-            for (int i = 0; i < 3; ++i) lx[r][i] = *reinterpret_cast<const f16x4 *>(xr + 256 * i + 4 * lane);
-        }
+        // normalized as the LayerNorm kernel does, written where the direct-to-LDS load would have put them
+        f16x4 o[4][3];
+        ln_rows768<4>(lx, lg, lb, o);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int row = wave + 4 * r;
-            f16x4 o[3];
-            ln_row768(lx[r], lg, lb, o);
 #pragma unroll
             for (int i = 0; i < 3; ++i)   // element 256 i + 4 lane: k-tile 4 i + lane / 16, chunk (lane & 15) / 2
                 *reinterpret_cast<f16x4 *>(xs + (4 * i + (lane >> 4)) * SKN_TILE + row * 128 +
-                                           ((((lane & 15) >> 1) ^ (row & 7)) << 4) + (lane & 1) * 8) = o[i];
+                                           ((((lane & 15) >> 1) ^ (row & 7)) << 4) + (lane & 1) * 8) = o[r][i];
         }
     } else {
         // load q (two per k-tile) fills rows 8 (q & 1) .. +7 of tile q / 2, lane l slot l & 7 of row
@@ -119,16 +135,22 @@ __global__ __launch_bounds__(64 * SKN_W) void k_gemm_skinny(uint16_t *__restrict
             __builtin_amdgcn_global_load_lds(src, G2_LDS(xs + q * 1024), 16, 0, 0);
         }
     }
-    wait_vm<0>();      // this wave's W, epilogue operands and A-block loads have landed
-    lds_barrier();     // ... and every wave's
+    // the direct-to-LDS A block is complete when this wave's loads have all landed (the LayerNorm
+    // path wrote its rows with LDS stores); the barrier then publishes every wave's part
+    if constexpr (!LNP) wait_vm<0>();
+    lds_barrier();
+    // the weights are used from here on (the compiler would otherwise widen INT8 codes inside the
+    // LayerNorm prologue, waiting there for the weight stream)
+#pragma unroll
+    for (int i = 0; i < NL; ++i) asm volatile("" : "+v"(wl[i]));
 
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         f16x8 w;
         if constexpr (QW) {
-            const uint4 v = wl[s >> 1];
-            w = i8x8_to_f16x8((s & 1) ? uint2{v.z, v.w} : uint2{v.x, v.y});
+            const i32x4 v = wl[s >> 1];
+            w = i8x8_to_f16x8((s & 1) ? uint2{(uint32_t)v[2], (uint32_t)v[3]} : uint2{(uint32_t)v[0], (uint32_t)v[1]});
         } else {
             w = __builtin_bit_cast(f16x8, wl[s]);
         }
