@@ -15,8 +15,10 @@
 //     waves' sums added in LDS in wave order, and wave 0's epilogue: scale (INT8), bias, then the
 //     elementwise op as the unfused sequence would apply it (epi_out).
 //   * The LayerNorm prologue (QKV after LN1, fc after LN2) normalizes the block's 16 rows with the
-//     LayerNorm kernel's arithmetic (ln_row768), so the result is bit-identical to the LayerNorm
-//     launch followed by this kernel.
+//     LayerNorm kernel's arithmetic (ln_rows768: ln_row768's operations row by row, the rows'
+//     reductions interleaved), so the result is bit-identical to the LayerNorm launch followed by
+//     this kernel.  Its rows are loaded before the weights and normalized while the weight stream
+//     is in flight.
 #include "common.h"
 
 namespace g2 {
