@@ -34,6 +34,7 @@ struct PDArgs {
 struct PDPlan {
     PDArgs args;
     bool q8;                          // int8 layer matrices (else fp16)
+    bool qa;                          // the q/k/v GEMV on the matrix cores (else v_dot2 from LDS)
 };
 
 // Builds the step's argument block; false when the backend or weights need the multi-kernel step.

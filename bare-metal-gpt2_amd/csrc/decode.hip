@@ -400,8 +400,65 @@ __device__ __forceinline__ void stage_qkv_q8(char *lds_w, const void *W, int h, 
     }
 }
 
-// Q8: every layer matrix is int8 codes with per-row scales (else every one is fp16).
+// The q/k/v GEMV on the matrix cores, its weights held in accumulation registers (AGPRs).  The QR rows
+// are QB blocks of 16 (v_mfma_f32_16x16x32_f16 A-fragments); wave w takes elements [192w, 192w + 192)
+// of every row in QS k-steps of 32, so the GEMV is QB * QS MFMAs per wave and a four-way sum.  Lane l
+// holds, for block b and k-step s, row 16b + (l & 15) at elements qk_k(w, s, l) .. +7 (k-steps paired
+// so that a lane's two chunks of a pair are 16 consecutive elements: one 16-byte load of int8 codes).
+// The B operand is the normalized x at the same elements in every column, so every column of D holds
+// the GEMV.  These registers are otherwise unused by the attention work-groups, and reading the
+// fragments from them instead of from LDS removes the q/k/v rows' 147 KB of LDS reads per layer.
+constexpr int QB = QR / 16;                       // row blocks
+constexpr int QKW = PD_E / 4;                     // elements of K per wave
+constexpr int QS = QKW / 32;                      // k-steps per wave
+static_assert(QR % 16 == 0 && QKW % 64 == 0, "whole blocks and whole k-step pairs");
+__device__ __forceinline__ int qk_k(int wave, int s, int lane) {
+    return QKW * wave + 64 * (s >> 1) + 16 * (lane >> 4) + 8 * (s & 1);
+}
+
+// Loads this wave's fragments of the QR rows (exact fp16; int8 codes widened) and moves them to the
+// accumulation registers.  Called when the attention work-group is idle (after its words of a layer
+// went out, before the next x arrives), so the wait for the loads costs nothing on the critical path.
+// The loads are all issued before the first is consumed (the compiler barrier keeps them there).
 template <bool Q8>
+__device__ __forceinline__ void stage_qkv_acc(i32x4 (&wq)[QB * QS], const void *W, int h, int sp, int wave, int lane) {
+    const int r = lane & 15;
+    if constexpr (Q8) {
+        const int8_t *Wb = reinterpret_cast<const int8_t *>(W);
+        i32x4 c[QB * QS / 2];
+#pragma unroll
+        for (int b = 0; b < QB; ++b)
+#pragma unroll
+            for (int p = 0; p < QS / 2; ++p)
+                c[b * QS / 2 + p] =
+                    *reinterpret_cast<const i32x4 *>(Wb + (size_t)qkv_row(h, sp, 16 * b + r) * PD_E + qk_k(wave, 2 * p, lane));
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < QB * QS / 2; ++i) {
+            const i32x4 v = c[i];
+            const i32x4 lo = __builtin_bit_cast(i32x4, i8x8_to_f16x8(uint2{(uint32_t)v[0], (uint32_t)v[1]}));
+            const i32x4 hi = __builtin_bit_cast(i32x4, i8x8_to_f16x8(uint2{(uint32_t)v[2], (uint32_t)v[3]}));
+            asm volatile("" : "=a"(wq[2 * i]) : "0"(lo));
+            asm volatile("" : "=a"(wq[2 * i + 1]) : "0"(hi));
+        }
+    } else {
+        const uint16_t *Wh = reinterpret_cast<const uint16_t *>(W);
+        i32x4 v[QB * QS];
+#pragma unroll
+        for (int b = 0; b < QB; ++b)
+#pragma unroll
+            for (int s = 0; s < QS; ++s)
+                v[b * QS + s] =
+                    *reinterpret_cast<const i32x4 *>(Wh + (size_t)qkv_row(h, sp, 16 * b + r) * PD_E + qk_k(wave, s, lane));
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < QB * QS; ++i) asm volatile("" : "=a"(wq[i]) : "0"(v[i]));
+    }
+}
+
+// Q8: every layer matrix is int8 codes with per-row scales (else every one is fp16).  QA: the q/k/v
+// GEMV on the matrix cores from accumulation registers (else v_dot2 from rows staged in LDS).
+template <bool Q8, bool QA>
 __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     using LY = Lds<Q8>;
     __shared__ __attribute__((aligned(1024))) char lds[LY::BYTES];
@@ -482,7 +539,9 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
         // Layer 0's keys and values go out before its weight rows, so their latency overlaps the
         // staging (later layers load theirs while waiting for x).
         load_kv(0);
-        if constexpr (Q8) stage_qkv_q8(ldw, a.layers[0].w[0], h, sp, tid);
+        i32x4 wq[QA ? QB * QS : 1];
+        if constexpr (QA) stage_qkv_acc<Q8>(wq, a.layers[0].w[0], h, sp, wave, lane);
+        else if constexpr (Q8) stage_qkv_q8(ldw, a.layers[0].w[0], h, sp, tid);
         else dma_qkv<LY::RB>(ldw, a.layers[0].w[0], h, sp, wave, lane);
         for (int l = 0; l < GPT2_N_LAYER; ++l) {
             const PDLayer &ly = a.layers[l];
@@ -511,14 +570,41 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             // This wave's weight DMA (fp16 weights) has landed (all waves: the barrier below).  It was
             // issued before everything since, so all but the last XR operations is enough: those are
             // the poll round of x still in flight, which need not be waited for.
-            wait_vm<XR>();
+            if constexpr (!QA) wait_vm<XR>();
             if (l == 1) mark(113);
-            if (tid < QR) {
+            if (!QA && tid < QR) {
                 qs[tid] = rs;
                 qb[tid] = h2f(rb);
             }
             layernorm768(xn, xs, lnp, lane);   // ends with a barrier
             if (l == 1) mark(114);
+            if constexpr (QA) {
+                // QB * QS MFMAs per wave over its K range; lanes 0, 16, 32, 48 (column 0 of D) hold rows
+                // 16b + 4(l / 16) .. +3 of block b; the four waves' partials are summed in wave order.
+                f16x8 xv[QS];
+#pragma unroll
+                for (int s2 = 0; s2 < QS; ++s2) xv[s2] = *reinterpret_cast<const f16x8 *>(xn + qk_k(wave, s2, lane));
+                f32x4 acc[QB];
+#pragma unroll
+                for (int b = 0; b < QB; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s2 = 0; s2 < QS; ++s2)
+#pragma unroll
+                    for (int b = 0; b < QB; ++b)
+                        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, wq[b * QS + s2]), xv[s2],
+                                                                        acc[b], 0, 0, 0);
+                float *red = reinterpret_cast<float *>(ldw);   // [4][QR], free until the attention scratch
+                if ((lane & 15) == 0) {
+#pragma unroll
+                    for (int b = 0; b < QB; ++b)
+                        *reinterpret_cast<f32x4 *>(red + wave * QR + 16 * b + 4 * (lane >> 4)) = acc[b];
+                }
+                lds_barrier();
+                if (tid < QR) {
+                    const float v = ((red[tid] + red[QR + tid]) + red[2 * QR + tid]) + red[3 * QR + tid];
+                    qkvh[tid] = (f16)(v * rs + h2f(rb));
+                }
+            } else {
             // ---- the QR rows: 16 lanes per row, 4 rows per wave per pass, two passes at a time.  Lane
             // j reads six 8-element fp16 chunks of each row; for int8 weights the chunks follow the
             // int8 layout (16 consecutive codes per 16-byte chunk j + 16i), so the products are summed
@@ -558,6 +644,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                         qkvh[rb2] = (f16)(ab * qs[rb2] + qb[rb2]);
                     }
                 }
+            }
             }
             lds_barrier();
             if (l == 1) mark(115);
@@ -661,7 +748,8 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             lds_barrier();   // the attention scratch (aliasing the weights) is free again
             mark(4 * l);
             if (l + 1 < GPT2_N_LAYER) {
-                if constexpr (Q8) stage_qkv_q8(ldw, a.layers[l + 1].w[0], h, sp, tid);
+                if constexpr (QA) stage_qkv_acc<Q8>(wq, a.layers[l + 1].w[0], h, sp, wave, lane);
+                else if constexpr (Q8) stage_qkv_q8(ldw, a.layers[l + 1].w[0], h, sp, tid);
                 else dma_qkv<LY::RB>(ldw, a.layers[l + 1].w[0], h, sp, wave, lane);
             }
         }
@@ -941,15 +1029,19 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
 // ------------------------------------------------------------------------------ host side
 static int g_pd_spin = PD_SPIN;
 static unsigned long long *g_pd_trace = nullptr;
+static int g_pd_qa = 1;   // q/k/v GEMV on the matrix cores (1) or v_dot2 from LDS (0), for new plans
+
+typedef void (*PDKernel)(PDArgs);
+static const PDKernel kPersist[2][2] = {{k_decode_persist<false, false>, k_decode_persist<false, true>},
+                                        {k_decode_persist<true, false>, k_decode_persist<true, true>}};
 
 // The step's work-groups wait on each other's words, so all PD_G of them must be resident at once:
 // the device must hold PD_G of them (one per CU with this LDS footprint) side by side.
-static bool persist_fits(bool q8) {
+static bool persist_fits(PDKernel k) {
     int dev = 0, ncu = 0, per = 0;
     if (hipGetDevice(&dev) != hipSuccess) return false;
     if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
-    const hipError_t e = q8 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_decode_persist<true>, PD_T, 0)
-                            : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_decode_persist<false>, PD_T, 0);
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, PD_T, 0);
     return e == hipSuccess && (long)per * ncu >= PD_G;
 }
 
@@ -989,7 +1081,8 @@ bool persist_plan(PDPlan &p, const GPT2Backend *be, const GPT2WeightsGPU *w, GPT
     if (nq != 0 && nq != 4 * GPT2_N_LAYER) return false;
     if (kv->maxT > GPT2_N_CTX) return false;   // an attention wave holds at most 64 keys
     p.q8 = nq != 0;
-    if (!persist_fits(p.q8)) return false;
+    p.qa = g_pd_qa != 0;
+    if (!persist_fits(kPersist[p.q8][p.qa])) return false;
     a.wte = w->wte;
     a.wpe = w->wpe;
     a.lnf_g = w->lnf_g;
@@ -1009,8 +1102,7 @@ bool persist_plan(PDPlan &p, const GPT2Backend *be, const GPT2WeightsGPU *w, GPT
 }
 
 void persist_launch(const PDPlan &p, hipStream_t s) {
-    if (p.q8) hipLaunchKernelGGL(k_decode_persist<true>, dim3(PD_G), dim3(PD_T), 0, s, p.args);
-    else hipLaunchKernelGGL(k_decode_persist<false>, dim3(PD_G), dim3(PD_T), 0, s, p.args);
+    hipLaunchKernelGGL(kPersist[p.q8][p.qa], dim3(PD_G), dim3(PD_T), 0, s, p.args);
 }
 
 size_t persist_ll_bytes() { return (size_t)LL_WORDS * 8; }
@@ -1024,6 +1116,9 @@ int persist_spin() { return g_pd_spin; }
 // that finds a word missing).  A tiny value
 // forces the timeout path with every kernel still exiting normally.
 extern "C" void gpt2_tune_decode_spin(int rounds) { g2::g_pd_spin = rounds >= 0 ? rounds : g2::PD_SPIN; }
+// Tuning / test hook: the persistent step's q/k/v GEMV for graphs created afterwards: 1 on the matrix
+// cores from accumulation registers, 0 v_dot2 over rows staged in LDS, < 0 the default (1).
+extern "C" void gpt2_tune_decode_qkv_mfma(int on) { g2::g_pd_qa = on < 0 ? 1 : (on != 0); }
 // Profiling hook: graphs created afterwards record, per work-group, the end time of every phase of
 // the persistent step (s_memrealtime, 100 MHz) into trace[wg * 128 + phase]: 4*l + {0 LN1 + q/k/v +
 // attention, 1 proj, 2 fc, 3 mlp-proj}, 60 head start, 61 head end, 62 step end, 63 step start, and
