@@ -29,6 +29,8 @@ struct PDArgs {
     uint64_t *ll;                     // exchange arena, LL_WORDS words
     int *err;                         // nonzero after a poll timed out
     unsigned long long *trace;        // optional: [G][128] phase times (100 MHz clock)
+    unsigned hold[3];                 // poll hold-offs (10 ns ticks): attention words, x, gelu(fc)
+    int var;                          // measurement variants (bits; 0 = the default code paths)
 };
 
 struct PDPlan {

@@ -456,6 +456,32 @@ __device__ __forceinline__ void stage_qkv_acc(i32x4 (&wq)[QB * QS], const void *
     }
 }
 
+// A GEMV work-group's RF = 16 fc rows as one block of MFMA A-fragments, k-steps laid out as in the
+// q/k/v GEMV (wave w: elements [192w, 192w + 192)): fp16, six 16-byte fragments per lane; int8, three
+// 16-byte groups of 16 codes, widened when used.  Threads 0-15 also hold their row's scale and bias.
+static_assert(RF == 16, "the fc rows of a work-group are one 16-row MFMA block");
+template <bool Q8>
+struct FcW {
+    i32x4 w[Q8 ? QS / 2 : QS];
+    float s;
+    uint16_t b;   // fp16 bits
+};
+template <bool Q8>
+__device__ __forceinline__ void load_fc(FcW<Q8> &F, const void *W, const float *S, const uint16_t *B, int r0, int wave,
+                                        int lane) {
+    const int row = r0 + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < (Q8 ? QS / 2 : QS); ++i) {
+        const int k = qk_k(wave, Q8 ? 2 * i : i, lane);
+        F.w[i] = Q8 ? *reinterpret_cast<const i32x4 *>(reinterpret_cast<const int8_t *>(W) + (size_t)row * PD_E + k)
+                    : *reinterpret_cast<const i32x4 *>(reinterpret_cast<const uint16_t *>(W) + (size_t)row * PD_E + k);
+    }
+    if (threadIdx.x < RF) {
+        F.s = Q8 ? S[r0 + threadIdx.x] : 1.f;
+        F.b = B[r0 + threadIdx.x];
+    }
+}
+
 // Q8: every layer matrix is int8 codes with per-row scales (else every one is fp16).  QA: the q/k/v
 // GEMV on the matrix cores from accumulation registers (else v_dot2 from rows staged in LDS).
 template <bool Q8, bool QA>
@@ -470,7 +496,8 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     uint16_t *hout = reinterpret_cast<uint16_t *>(lds + LDS_MISC + 64);   // RF values
     int *wflag = reinterpret_cast<int *>(lds + LDS_MISC + 96);             // ll_read verdicts, 4 ints
     uint32_t *xout = reinterpret_cast<uint32_t *>(lds + LDS_MISC + 112);   // RP x words, one store
-    static_assert(64 + 2 * RF <= 96 && 112 + 4 * RP <= 512, "LDS misc layout");
+    // misc + 128: the q.k_pos part (attention work-groups); + 256: the heads' weights (GEMV work-groups)
+    static_assert(64 + 2 * RF <= 96 && 112 + 4 * RP <= 128 && 256 + 4 * 16 * 4 <= 512, "LDS misc layout");
 
     // wave < 4 made explicit (PD_T = 256): a wave's share of GEMV rows (wave + 4j < ROWS) is then
     // known at compile time, with no branch around the row dot products ahead of their reductions.
@@ -687,6 +714,23 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             }
 #pragma unroll
             for (int e = 0; e < 8; ++e) cl[wave][dg + e][slot] = cacc[e];
+            // Each wave sums its eight slots of every dimension itself (lane = dimension; its own
+            // LDS writes above come first, in order), and wave 3 (the fewest keys) forms this
+            // split's part of q.k_pos, so the merge below reads one value per wave and dimension.
+            float *cs = &pl[wave][0];   // the wave's softmax scratch, free again
+            float *sdot = reinterpret_cast<float *>(lds + LDS_MISC + 128);
+            if (!(a.var & 2)) {
+                const float4 ca = *reinterpret_cast<const float4 *>(&cl[wave][lane][0]);
+                const float4 cb = *reinterpret_cast<const float4 *>(&cl[wave][lane][4]);
+                cs[lane] = ((ca.x + ca.y) + (ca.z + ca.w)) + ((cb.x + cb.y) + (cb.z + cb.w));
+                if (tid == 3 * 64) {
+                    // q[KS*sp ..] . k_pos[KS*sp ..] in fp32 from the fp16 values
+                    float d = 0.f;
+#pragma unroll
+                    for (int i = 0; i < KS; ++i) d += (float)qkvh[KS * sp + i] * (float)qkvh[PD_D + i];
+                    *sdot = d;
+                }
+            }
             if (lane == 0) {
                 sm[wave] = m_w;
                 sl[wave] = l_w;
@@ -720,6 +764,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                     } else {
                         const int d0 = 2 * (tid - AW_C);
                         float c2[2] = {0.f, 0.f};
+                        if (a.var & 2) {
 #pragma unroll
                         for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
@@ -728,15 +773,24 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                                 const float4 cb = *reinterpret_cast<const float4 *>(&cl[w][d0 + h2][4]);
                                 c2[h2] += (((ca.x + ca.y) + (ca.z + ca.w)) + ((cb.x + cb.y) + (cb.z + cb.w))) * fw[w];
                             }
+                        } else {
+#pragma unroll
+                        for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+                            for (int w = 0; w < 4; ++w) c2[h2] += pl[w][d0 + h2] * fw[w];
+                        }
                         const float inv = lsum != 0.f ? 1.0f / lsum : 0.f;
                         val = (uint32_t)f2h(c2[0] * inv) | ((uint32_t)f2h(c2[1] * inv) << 16);
                     }
                 } else if (tid == AW_S) {
-                    // q[KS*sp ..] . k_pos[KS*sp ..] in fp32 from the fp16 values
+                    if (a.var & 2) {
                     float d = 0.f;
 #pragma unroll
                     for (int i = 0; i < KS; ++i) d += (float)qkvh[KS * sp + i] * (float)qkvh[PD_D + i];
                     val = __float_as_uint(d);
+                    } else {
+                    val = __float_as_uint(*sdot);
+                    }
                 } else {
                     const int i = 2 * (tid - AW_V);
                     val = (uint32_t)__builtin_bit_cast(uint16_t, qkvh[PD_D + KS + i]) |
@@ -775,17 +829,20 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
         // order, so a weight load issued shortly before a poll would hold that poll back.
         PhaseW<768, Q8, RP> WP;
         PhaseW<768, Q8, RF> WF;
+        FcW<Q8> FC;
+        const bool fc_dot = a.var & 4;   // fc by v_dot2 rows (else one MFMA block)
         PhaseW<3072, Q8, RM> WM;
         LNParams lnp;
         load_phase(WP, a.layers[0].w[1], a.layers[0].s[1], a.layers[0].b[1], g * RP, wave, lane);
-        load_phase(WF, a.layers[0].w[2], a.layers[0].s[2], a.layers[0].b[2], g * RF, wave, lane);
+        if (fc_dot) load_phase(WF, a.layers[0].w[2], a.layers[0].s[2], a.layers[0].b[2], g * RF, wave, lane);
+        else load_fc(FC, a.layers[0].w[2], a.layers[0].s[2], a.layers[0].b[2], g * RF, wave, lane);
         load_ln(lnp, a.layers[0].ln2_g, a.layers[0].ln2_b);
         load_phase(WM, a.layers[0].w[3], a.layers[0].s[3], a.layers[0].b[3], g * RM, wave, lane);
         unsigned long long t_st = __builtin_amdgcn_s_memrealtime();   // this work-group's last store
         for (int l = 0; l < GPT2_N_LAYER; ++l) {
             // ---- P: combine the attention words, proj rows, + bias + residual
             constexpr int NA = PD_NA * PD_PW;
-            hold_until(t_st + PD_HOLD_ATT);
+            hold_until(t_st + a.hold[0]);
             if (!ll_read<(NA + PD_T - 1) / PD_T>(LA, NA, seq(4 * l), a.err, spin, wflag, at_word,
                                                  [&](int i, uint32_t d) { part[i] = __uint_as_float(d); }))
                 return;
@@ -802,6 +859,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 const uint32_t u = __float_as_uint(w);
                 return h2f((uint16_t)(hi ? u >> 16 : u & 0xffff));
             };
+            if (a.var & 1) {
 #pragma unroll
             for (int i = 0; i < 3; ++i) {
                 const int e = tid + PD_T * i, hh = e / PD_D, d = e % PD_D;
@@ -830,6 +888,47 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 }
                 xn[e] = (f16)(c / L);
             }
+            } else {
+            // The heads' weights first: lanes 0-14 of wave w form, for heads w, w + 4, w + 8, the five
+            // parts' weights (four splits and the new key) normalized by the head's total, into LDS;
+            // the wave's own reads of them below come after its writes (in order), so no barrier.
+            // Then each element is five products: sum over parts of (c / l of the part) x weight.
+            float *hw = reinterpret_cast<float *>(lds + LDS_MISC + 256) + wave * 16;   // [3][5]
+            if (lane < 15) {
+                const int hl = lane / 5, j = lane - 5 * hl;
+                const float *p = part + (wave + 4 * hl) * PD_S * PD_PW;
+                float m4[PD_S], l4[PD_S], s4[PD_S], f4[PD_S];
+#pragma unroll
+                for (int s2 = 0; s2 < PD_S; ++s2) {
+                    m4[s2] = p[s2 * PD_PW + AW_M];
+                    l4[s2] = p[s2 * PD_PW + AW_L];
+                    s4[s2] = p[s2 * PD_PW + AW_S];
+                }
+                const float spos = ((s4[0] + s4[1]) + (s4[2] + s4[3])) * 0.125f;
+                float mx = spos;
+#pragma unroll
+                for (int s2 = 0; s2 < PD_S; ++s2) mx = (l4[s2] != 0.f) ? fmaxf(mx, m4[s2]) : mx;
+#pragma unroll
+                for (int s2 = 0; s2 < PD_S; ++s2) f4[s2] = (l4[s2] != 0.f) ? __expf(m4[s2] - mx) * l4[s2] : 0.f;
+                const float fpos = __expf(spos - mx);
+                float L = fpos, fj = fpos;
+#pragma unroll
+                for (int s2 = 0; s2 < PD_S; ++s2) {
+                    L += f4[s2];
+                    fj = (j == s2) ? f4[s2] : fj;
+                }
+                hw[lane] = fj * __builtin_amdgcn_rcpf(L);
+            }
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                const int e = tid + PD_T * i, hh = e / PD_D, d = e % PD_D;
+                const float *p = part + hh * PD_S * PD_PW;
+                float c = half_of(p[(d / KS) * PD_PW + AW_V + (d % KS) / 2], d & 1) * hw[5 * i + PD_S];
+#pragma unroll
+                for (int s2 = 0; s2 < PD_S; ++s2) c += half_of(p[s2 * PD_PW + AW_C + d / 2], d & 1) * hw[5 * i + s2];
+                xn[e] = (f16)c;
+            }
+            }
             if (l == 1) mark(118);
             lds_barrier();
             if (l == 1) mark(119);
@@ -842,14 +941,39 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             t_st = __builtin_amdgcn_s_memrealtime();
             mark(4 * l + 1);
             // ---- F: LN2 + fc rows [g*RF, +RF) + gelu, exchanged in pairs
-            hold_until(t_st + PD_HOLD_X);
+            hold_until(t_st + a.hold[1]);
             if (!read_x(seq(4 * l + 1))) return;
             mark(64 + 4 * l + 2);
             layernorm768(xn, xs, lnp, lane);
             if (l == 1) mark(120);
-            run_phase(WF, xn, wave, lane, [&](int k, float v) {
-                if (lane == 0) hout[k] = __builtin_bit_cast(uint16_t, (f16)gelu_tanh(v));
-            });
+            if (fc_dot) {
+                run_phase(WF, xn, wave, lane, [&](int k, float v) {
+                    if (lane == 0) hout[k] = __builtin_bit_cast(uint16_t, (f16)gelu_tanh(v));
+                });
+            } else {
+                // QS MFMAs per wave over its K range; column 0 of D (lanes 0, 16, 32, 48) holds rows
+                // 4(l / 16) .. +3; the four waves' partials are summed in wave order by threads 0-15.
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s2 = 0; s2 < QS; ++s2) {
+                    const f16x8 xv = *reinterpret_cast<const f16x8 *>(xn + qk_k(wave, s2, lane));
+                    f16x8 wv;
+                    if constexpr (Q8) {
+                        const i32x4 c = FC.w[s2 >> 1];
+                        wv = i8x8_to_f16x8((s2 & 1) ? uint2{(uint32_t)c[2], (uint32_t)c[3]} : uint2{(uint32_t)c[0], (uint32_t)c[1]});
+                    } else {
+                        wv = __builtin_bit_cast(f16x8, FC.w[s2]);
+                    }
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv, xv, acc, 0, 0, 0);
+                }
+                float *red = part;   // the attention words are combined by now
+                if ((lane & 15) == 0) *reinterpret_cast<f32x4 *>(red + wave * RF + 4 * (lane >> 4)) = acc;
+                lds_barrier();
+                if (tid < RF) {
+                    const float v = ((red[tid] + red[RF + tid]) + red[2 * RF + tid]) + red[3 * RF + tid];
+                    hout[tid] = __builtin_bit_cast(uint16_t, (f16)gelu_tanh(v * FC.s + h2f(FC.b)));
+                }
+            }
             if (l == 1) mark(121);
             lds_barrier();
             if (tid < RF / 2)
@@ -857,7 +981,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             t_st = __builtin_amdgcn_s_memrealtime();
             mark(4 * l + 2);
             // ---- M: mlp-proj rows [g*RM, +RM) over gelu(fc), + bias + residual
-            hold_until(t_st + PD_HOLD_HID);
+            hold_until(t_st + a.hold[2]);
             if (!ll_read<PD_F / 2 / PD_T>(LHd, PD_F / 2, seq(4 * l + 2), a.err, spin, wflag, hd_word,
                                           [&](int i, uint32_t d) {
                                               hs[2 * i] = __builtin_bit_cast(f16, (uint16_t)(d & 0xffff));
@@ -869,7 +993,8 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             if (next) {
                 const PDLayer &ln = a.layers[l + 1];
                 load_phase(WP, ln.w[1], ln.s[1], ln.b[1], g * RP, wave, lane);
-                load_phase(WF, ln.w[2], ln.s[2], ln.b[2], g * RF, wave, lane);
+                if (fc_dot) load_phase(WF, ln.w[2], ln.s[2], ln.b[2], g * RF, wave, lane);
+                else load_fc(FC, ln.w[2], ln.s[2], ln.b[2], g * RF, wave, lane);
                 load_ln(lnp, ln.ln2_g, ln.ln2_b);
             }
             run_phase(WM, hs, wave, lane, [&](int k, float v) {
@@ -1030,6 +1155,8 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
 static int g_pd_spin = PD_SPIN;
 static unsigned long long *g_pd_trace = nullptr;
 static int g_pd_qa = 1;   // q/k/v GEMV on the matrix cores (1) or v_dot2 from LDS (0), for new plans
+static int g_pd_hold[3] = {-1, -1, -1};   // hold-off overrides for new plans (< 0: the constant)
+static int g_pd_var = 0;                  // measurement variant bits for new plans
 
 typedef void (*PDKernel)(PDArgs);
 static const PDKernel kPersist[2][2] = {{k_decode_persist<false, false>, k_decode_persist<false, true>},
@@ -1098,6 +1225,9 @@ bool persist_plan(PDPlan &p, const GPT2Backend *be, const GPT2WeightsGPU *w, GPT
     a.ll = ll;
     a.err = err;
     a.trace = g_pd_trace;
+    const unsigned hold0[3] = {PD_HOLD_ATT, PD_HOLD_X, PD_HOLD_HID};
+    for (int i = 0; i < 3; ++i) a.hold[i] = g_pd_hold[i] >= 0 ? (unsigned)g_pd_hold[i] : hold0[i];
+    a.var = g_pd_var;
     return true;
 }
 
@@ -1119,6 +1249,16 @@ extern "C" void gpt2_tune_decode_spin(int rounds) { g2::g_pd_spin = rounds >= 0 
 // Tuning / test hook: the persistent step's q/k/v GEMV for graphs created afterwards: 1 on the matrix
 // cores from accumulation registers, 0 v_dot2 over rows staged in LDS, < 0 the default (1).
 extern "C" void gpt2_tune_decode_qkv_mfma(int on) { g2::g_pd_qa = on < 0 ? 1 : (on != 0); }
+// Tuning hook: the persistent step's poll hold-offs, in 10 ns ticks, for graphs created afterwards:
+// before the attention words, x after proj, gelu(fc); a value < 0 keeps that hold-off's default.
+// Measurement hook: variant bits of the persistent step for graphs created afterwards (0: the default
+// code paths; a set bit selects the previous form of one piece, kept for interleaved A/B).
+extern "C" void gpt2_tune_decode_variant(int bits) { g2::g_pd_var = bits; }
+extern "C" void gpt2_tune_decode_holds(int att, int x, int hid) {
+    g2::g_pd_hold[0] = att;
+    g2::g_pd_hold[1] = x;
+    g2::g_pd_hold[2] = hid;
+}
 // Profiling hook: graphs created afterwards record, per work-group, the end time of every phase of
 // the persistent step (s_memrealtime, 100 MHz) into trace[wg * 128 + phase]: 4*l + {0 LN1 + q/k/v +
 // attention, 1 proj, 2 fc, 3 mlp-proj}, 60 head start, 61 head end, 62 step end, 63 step start, and
