@@ -154,9 +154,7 @@ SIGNATURES = {
                                             C.POINTER(GPT2ScratchGPU), _vp, _vp, _i]),
     "gpt2_decode_graph_mode": (_i, [_vp]),
     "gpt2_tune_decode_spin": (None, [_i]),
-    "gpt2_tune_decode_qkv_mfma": (None, [_i]),
     "gpt2_tune_decode_holds": (None, [_i, _i, _i]),
-    "gpt2_tune_decode_variant": (None, [_i]),
     "gpt2_tune_decode_trace": (None, [_vp]),
     "gpt2_tune_prefill_fused": (None, [_i]),
     "gpt2_tune_prefill_lnfold": (None, [_i]),

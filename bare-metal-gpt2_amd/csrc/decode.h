@@ -30,13 +30,11 @@ struct PDArgs {
     int *err;                         // nonzero after a poll timed out
     unsigned long long *trace;        // optional: [G][128] phase times (100 MHz clock)
     unsigned hold[3];                 // poll hold-offs (10 ns ticks): attention words, x, gelu(fc)
-    int var;                          // measurement variants (bits; 0 = the default code paths)
 };
 
 struct PDPlan {
     PDArgs args;
     bool q8;                          // int8 layer matrices (else fp16)
-    bool qa;                          // the q/k/v GEMV on the matrix cores (else v_dot2 from LDS)
 };
 
 // Builds the step's argument block; false when the backend or weights need the multi-kernel step.

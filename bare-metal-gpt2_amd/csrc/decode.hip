@@ -100,33 +100,35 @@ constexpr int PD_SPIN = 1 << 15;                   // default poll rounds before
 // previous store.  A poll issued right after the work-group's own store, or long before the words
 // can arrive, slows the exchanges of the whole step (its loads wait behind the store's write-through
 // and load the memory side while the other work-groups' stores drain).  Measured per token at
-// ctx 512: 178.1 us with none, ~164 with these three; the attention words arrive >= 4.5 us after
-// the mlp-proj store at any position, x and gelu(fc) ~1.3-1.5 us after the store before them.
-constexpr unsigned PD_HOLD_ATT = 250;              // after the mlp-proj store, before the attention words
+// ctx 512 (interleaved A/B): 163.5 us with none against 156.3 with 2.5 / 0.6 / 0.5 us, and 300 / 60 /
+// 40 ticks 0.8% faster again; the attention words arrive ~4 us after the mlp-proj store, x and
+// gelu(fc) ~1.3 us after the store before them.  Holds that follow each layer's measured arrival
+// (the previous layer's arrival minus a margin of one to three poll rounds, up and down or only
+// down) measured 1-1.3% slower than these constants at every margin tried.  gpt2_tune_decode_holds
+// sets them per graph.
+constexpr unsigned PD_HOLD_ATT = 300;              // after the mlp-proj store, before the attention words
 constexpr unsigned PD_HOLD_X = 60;                 // after the proj store, before x
-constexpr unsigned PD_HOLD_HID = 50;               // after the fc store, before gelu(fc)
+constexpr unsigned PD_HOLD_HID = 40;               // after the fc store, before gelu(fc)
 // Phase numbers (sequence = epoch*64 + phase): per layer l, 4l attention, 4l+1 x after proj,
 // 4l+2 gelu(fc), 4l+3 x after mlp-proj; 48 head candidates.
 constexpr int PH_CAND = 4 * GPT2_N_LAYER;
 
-// LDS layout (bytes).  Common: xs, xn, argmax scratch.  Attention work-groups: the q/k/v weight rows
-// they compute (QR rows, always fp16: int8 rows are widened when they are staged), reused after the
-// GEMV for the attention scratch; GEMV work-groups: gelu(fc) and the attention words.
+// LDS layout (bytes).  Common: xs, xn, argmax scratch.  Attention work-groups: the four waves'
+// partial sums of the q/k/v GEMV, reused for the attention scratch, and q, the k slice and the v slice;
+// GEMV work-groups: gelu(fc) and the attention words (their space also takes the fc partial sums).
 constexpr int LDS_XS = 0, LDS_XN = LDS_XS + 2 * PD_E, LDS_MISC = LDS_XN + 2 * PD_E;   // misc: 512 B
 constexpr int LDS_ROLE = LDS_MISC + 512;
-template <bool Q8> struct Lds {
-    static constexpr int RB = 2 * PD_E;                   // bytes per q/k/v weight row (fp16)
-    static constexpr int W = LDS_ROLE;                    // A: q/k/v weights, QR * RB
-    static constexpr int QKVH = W + QR * RB;              // A: q, k slice, v slice (fp16)
-    static constexpr int QSB = QKVH + 2 * QR;             // A: their scales and biases (fp32)
-    static constexpr int CL = W;                          // A, after the GEMV: [4][64][8] fp32
+struct Lds {
+    static constexpr int RED = LDS_ROLE;                  // A: [4][QR] fp32 q/k/v partial sums
+    static constexpr int CL = LDS_ROLE;                   // A, after the GEMV: [4][64][8] fp32
     static constexpr int PL = CL + 4 * PD_D * 8 * 4;      // A, after the GEMV: [4][64] fp32
+    static constexpr int QKVH = PL + 4 * 64 * 4;          // A: q, k slice, v slice (fp16)
     static constexpr int HS = LDS_ROLE;                   // G: gelu(fc), 3072 fp16
     static constexpr int PART = HS + 2 * PD_F;            // G: NA*PW fp32
     static constexpr int CANDS = LDS_ROLE;                // head phase: G candidates
-    static constexpr int BYTES = QSB + 2 * 4 * QR;
-    static_assert(PART + 4 * PD_NA * PD_PW <= BYTES && PL + 4 * 4 * 64 <= QKVH, "LDS layout");
-    static_assert(BYTES <= 160 * 1024, "fits the 160 KB of LDS of a gfx950 CU");
+    static constexpr int BYTES_A = QKVH + 2 * QR, BYTES_G = PART + 4 * PD_NA * PD_PW;
+    static constexpr int BYTES = BYTES_A > BYTES_G ? BYTES_A : BYTES_G;
+    static_assert(RED + 4 * 4 * QR <= QKVH && CANDS + 4 * PD_G <= BYTES, "LDS layout");
 };
 
 __device__ __forceinline__ uint64_t ll_ld(const uint64_t *p) {
@@ -354,60 +356,15 @@ __device__ __forceinline__ int qkv_row(int h, int sp, int r) {
                     : (r < PD_D + KS ? PD_E : 2 * PD_E) + h * PD_D + KS * sp + ((r - PD_D) & (KS - 1));
 }
 
-// DMA of those QR weight rows (RB bytes each) into LDS, row-major: 1 KB per wave instruction, lane i
-// of instruction q landing at byte 1024q + 16i.
-template <int RB>
-__device__ __forceinline__ void dma_qkv(char *lds_w, const void *W, int h, int sp, int wave, int lane) {
-    constexpr int NINS = QR * RB / 1024;
-    static_assert(QR * RB % 1024 == 0 && RB % 16 == 0, "whole 1 KB DMA blocks of whole 16 B pieces");
-    const char *Wb = reinterpret_cast<const char *>(W);
-    for (int q = wave; q < NINS; q += 4) {
-        const int byte = q * 1024 + lane * 16, r = byte / RB, off = byte - r * RB;
-        __builtin_amdgcn_global_load_lds(Wb + (size_t)qkv_row(h, sp, r) * RB + off, G2_LDS(lds_w + q * 1024), 16, 0, 0);
-    }
-}
-
-// The same QR rows from int8 codes, widened to exact fp16 on the way into LDS (same layout as
-// dma_qkv's fp16 rows).  The attention work-groups are idle while the GEMV phases run, so the
-// widening costs nothing on the critical path and the q/k/v GEMV then reads fp16 like the fp16 path.
-// Thread t handles 16-byte chunks t + 256m (m < 18) of the QR x 768 codes; the loads are all in
-// flight before the first is widened.
-__device__ __forceinline__ void stage_qkv_q8(char *lds_w, const void *W, int h, int sp, int tid) {
-    constexpr int CH = PD_E / 16, NCH = QR * CH, PER = NCH / PD_T;
-    static_assert(NCH % PD_T == 0, "whole chunks per thread");
-    const int8_t *Wb = reinterpret_cast<const int8_t *>(W);
-    uint4 v[PER];
-#pragma unroll
-    for (int m = 0; m < PER; ++m) {
-        const int c = m * PD_T + tid, r = c / CH, k = c - r * CH;
-        v[m] = *reinterpret_cast<const uint4 *>(Wb + (size_t)qkv_row(h, sp, r) * PD_E + k * 16);
-    }
-#pragma unroll
-    for (int m = 0; m < PER; ++m) {
-        const int c = m * PD_T + tid, r = c / CH, k = c - r * CH;
-        const uint32_t wd[4] = {v[m].x, v[m].y, v[m].z, v[m].w};
-        uint32_t o[8];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            f16x2 lo, hi;
-            i8x4_to_f16x4_v(wd[t], lo, hi);
-            o[2 * t] = __builtin_bit_cast(uint32_t, lo);
-            o[2 * t + 1] = __builtin_bit_cast(uint32_t, hi);
-        }
-        uint4 *dst = reinterpret_cast<uint4 *>(lds_w + r * 2 * PD_E + k * 32);
-        dst[0] = uint4{o[0], o[1], o[2], o[3]};
-        dst[1] = uint4{o[4], o[5], o[6], o[7]};
-    }
-}
-
 // The q/k/v GEMV on the matrix cores, its weights held in accumulation registers (AGPRs).  The QR rows
 // are QB blocks of 16 (v_mfma_f32_16x16x32_f16 A-fragments); wave w takes elements [192w, 192w + 192)
 // of every row in QS k-steps of 32, so the GEMV is QB * QS MFMAs per wave and a four-way sum.  Lane l
 // holds, for block b and k-step s, row 16b + (l & 15) at elements qk_k(w, s, l) .. +7 (k-steps paired
 // so that a lane's two chunks of a pair are 16 consecutive elements: one 16-byte load of int8 codes).
 // The B operand is the normalized x at the same elements in every column, so every column of D holds
-// the GEMV.  These registers are otherwise unused by the attention work-groups, and reading the
-// fragments from them instead of from LDS removes the q/k/v rows' 147 KB of LDS reads per layer.
+// the GEMV.  These registers are otherwise unused by the attention work-groups; held there, the
+// fragments cost no LDS reads (staged in LDS, the QR rows were 147 KB of LDS reads per layer: 163.7
+// against 156.6 us per token, INT8, interleaved A/B).
 constexpr int QB = QR / 16;                       // row blocks
 constexpr int QKW = PD_E / 4;                     // elements of K per wave
 constexpr int QS = QKW / 32;                      // k-steps per wave
@@ -482,11 +439,10 @@ __device__ __forceinline__ void load_fc(FcW<Q8> &F, const void *W, const float *
     }
 }
 
-// Q8: every layer matrix is int8 codes with per-row scales (else every one is fp16).  QA: the q/k/v
-// GEMV on the matrix cores from accumulation registers (else v_dot2 from rows staged in LDS).
-template <bool Q8, bool QA>
+// Q8: every layer matrix is int8 codes with per-row scales (else every one is fp16).
+template <bool Q8>
 __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
-    using LY = Lds<Q8>;
+    using LY = Lds;
     __shared__ __attribute__((aligned(1024))) char lds[LY::BYTES];
     f16 *xs = reinterpret_cast<f16 *>(lds + LDS_XS);      // current residual stream
     f16 *xn = reinterpret_cast<f16 *>(lds + LDS_XN);      // normalized input / attention output
@@ -534,9 +490,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
         const int pw = (j1 - j0 + 3) / 4;                  // keys per wave, <= 64 (maxT <= N_CTX)
         const int w0 = min(j1, j0 + pw * wave), w1 = min(j1, w0 + pw);
         const int slot = lane >> 3, dg = (lane & 7) * 8;
-        char *ldw = lds + LY::W;
         f16 *qkvh = reinterpret_cast<f16 *>(lds + LY::QKVH);
-        float *qs = reinterpret_cast<float *>(lds + LY::QSB), *qb = qs + QR;
         float(*cl)[PD_D][8] = reinterpret_cast<float(*)[PD_D][8]>(lds + LY::CL);
         float(*pl)[64] = reinterpret_cast<float(*)[64]>(lds + LY::PL);
         // The embedding's loads go first: the memory counter completes in issue order, so loads
@@ -566,10 +520,8 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
         // Layer 0's keys and values go out before its weight rows, so their latency overlaps the
         // staging (later layers load theirs while waiting for x).
         load_kv(0);
-        i32x4 wq[QA ? QB * QS : 1];
-        if constexpr (QA) stage_qkv_acc<Q8>(wq, a.layers[0].w[0], h, sp, wave, lane);
-        else if constexpr (Q8) stage_qkv_q8(ldw, a.layers[0].w[0], h, sp, tid);
-        else dma_qkv<LY::RB>(ldw, a.layers[0].w[0], h, sp, wave, lane);
+        i32x4 wq[QB * QS];   // this wave's q/k/v fragments, in accumulation registers
+        stage_qkv_acc<Q8>(wq, a.layers[0].w[0], h, sp, wave, lane);
         for (int l = 0; l < GPT2_N_LAYER; ++l) {
             const PDLayer &ly = a.layers[l];
             uint16_t *Kc = a.kv + (size_t)(2 * l) * PD_H * hstride + h * hstride;
@@ -594,18 +546,10 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 return;
             }
             mark(64 + 4 * l);
-            // This wave's weight DMA (fp16 weights) has landed (all waves: the barrier below).  It was
-            // issued before everything since, so all but the last XR operations is enough: those are
-            // the poll round of x still in flight, which need not be waited for.
-            if constexpr (!QA) wait_vm<XR>();
             if (l == 1) mark(113);
-            if (!QA && tid < QR) {
-                qs[tid] = rs;
-                qb[tid] = h2f(rb);
-            }
             layernorm768(xn, xs, lnp, lane);   // ends with a barrier
             if (l == 1) mark(114);
-            if constexpr (QA) {
+            {
                 // QB * QS MFMAs per wave over its K range; lanes 0, 16, 32, 48 (column 0 of D) hold rows
                 // 16b + 4(l / 16) .. +3 of block b; the four waves' partials are summed in wave order.
                 f16x8 xv[QS];
@@ -620,7 +564,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                     for (int b = 0; b < QB; ++b)
                         acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, wq[b * QS + s2]), xv[s2],
                                                                         acc[b], 0, 0, 0);
-                float *red = reinterpret_cast<float *>(ldw);   // [4][QR], free until the attention scratch
+                float *red = reinterpret_cast<float *>(lds + LY::RED);   // free until the attention scratch
                 if ((lane & 15) == 0) {
 #pragma unroll
                     for (int b = 0; b < QB; ++b)
@@ -631,47 +575,6 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                     const float v = ((red[tid] + red[QR + tid]) + red[2 * QR + tid]) + red[3 * QR + tid];
                     qkvh[tid] = (f16)(v * rs + h2f(rb));
                 }
-            } else {
-            // ---- the QR rows: 16 lanes per row, 4 rows per wave per pass, two passes at a time.  Lane
-            // j reads six 8-element fp16 chunks of each row; for int8 weights the chunks follow the
-            // int8 layout (16 consecutive codes per 16-byte chunk j + 16i), so the products are summed
-            // in the same order as on the widened-in-registers path.
-            {
-                const int j = lane & 15, rsl = lane >> 4;
-                auto eoff = [&](int i) { return Q8 ? (j + 16 * (i >> 1)) * 16 + 8 * (i & 1) : (j + 16 * i) * 8; };
-                f16x8 xr[6];
-#pragma unroll
-                for (int i = 0; i < 6; ++i) xr[i] = *reinterpret_cast<const f16x8 *>(xn + eoff(i));
-                auto dot = [&](const uint4(&w)[6]) {
-                    float acc = 0.f;
-#pragma unroll
-                    for (int i = 0; i < 6; ++i) {
-                        const uint32_t wd[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
-#pragma unroll
-                        for (int t = 0; t < 4; ++t)
-                            acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, wd[t]), f16x2{xr[i][2 * t], xr[i][2 * t + 1]},
-                                                         acc, false);
-                    }
-                    return acc;
-                };
-#pragma unroll
-                for (int p = 0; p < QR / 16; p += 2) {
-                    const int ra = 16 * p + 4 * wave + rsl, rb2 = ra + 16;
-                    uint4 wa[6], wb[6];
-#pragma unroll
-                    for (int i = 0; i < 6; ++i) {
-                        wa[i] = *reinterpret_cast<const uint4 *>(ldw + ra * LY::RB + 2 * eoff(i));
-                        wb[i] = *reinterpret_cast<const uint4 *>(ldw + rb2 * LY::RB + 2 * eoff(i));
-                    }
-                    float aa = dot(wa), ab = dot(wb);
-                    aa = row16_sum(aa);
-                    ab = row16_sum(ab);
-                    if (j == 0) {
-                        qkvh[ra] = (f16)(aa * qs[ra] + qb[ra]);
-                        qkvh[rb2] = (f16)(ab * qs[rb2] + qb[rb2]);
-                    }
-                }
-            }
             }
             lds_barrier();
             if (l == 1) mark(115);
@@ -719,7 +622,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             // split's part of q.k_pos, so the merge below reads one value per wave and dimension.
             float *cs = &pl[wave][0];   // the wave's softmax scratch, free again
             float *sdot = reinterpret_cast<float *>(lds + LDS_MISC + 128);
-            if (!(a.var & 2)) {
+            {
                 const float4 ca = *reinterpret_cast<const float4 *>(&cl[wave][lane][0]);
                 const float4 cb = *reinterpret_cast<const float4 *>(&cl[wave][lane][4]);
                 cs[lane] = ((ca.x + ca.y) + (ca.z + ca.w)) + ((cb.x + cb.y) + (cb.z + cb.w));
@@ -764,33 +667,15 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                     } else {
                         const int d0 = 2 * (tid - AW_C);
                         float c2[2] = {0.f, 0.f};
-                        if (a.var & 2) {
-#pragma unroll
-                        for (int h2 = 0; h2 < 2; ++h2)
-#pragma unroll
-                            for (int w = 0; w < 4; ++w) {
-                                const float4 ca = *reinterpret_cast<const float4 *>(&cl[w][d0 + h2][0]);
-                                const float4 cb = *reinterpret_cast<const float4 *>(&cl[w][d0 + h2][4]);
-                                c2[h2] += (((ca.x + ca.y) + (ca.z + ca.w)) + ((cb.x + cb.y) + (cb.z + cb.w))) * fw[w];
-                            }
-                        } else {
 #pragma unroll
                         for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
                             for (int w = 0; w < 4; ++w) c2[h2] += pl[w][d0 + h2] * fw[w];
-                        }
                         const float inv = lsum != 0.f ? 1.0f / lsum : 0.f;
                         val = (uint32_t)f2h(c2[0] * inv) | ((uint32_t)f2h(c2[1] * inv) << 16);
                     }
                 } else if (tid == AW_S) {
-                    if (a.var & 2) {
-                    float d = 0.f;
-#pragma unroll
-                    for (int i = 0; i < KS; ++i) d += (float)qkvh[KS * sp + i] * (float)qkvh[PD_D + i];
-                    val = __float_as_uint(d);
-                    } else {
                     val = __float_as_uint(*sdot);
-                    }
                 } else {
                     const int i = 2 * (tid - AW_V);
                     val = (uint32_t)__builtin_bit_cast(uint16_t, qkvh[PD_D + KS + i]) |
@@ -799,12 +684,10 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 ll_st(LA + at_word(wg * PD_PW + tid), val, seq(4 * l));
             }
             if (l == 1) mark(118);
-            lds_barrier();   // the attention scratch (aliasing the weights) is free again
+            lds_barrier();   // the attention scratch is free again
             mark(4 * l);
             if (l + 1 < GPT2_N_LAYER) {
-                if constexpr (QA) stage_qkv_acc<Q8>(wq, a.layers[l + 1].w[0], h, sp, wave, lane);
-                else if constexpr (Q8) stage_qkv_q8(ldw, a.layers[l + 1].w[0], h, sp, tid);
-                else dma_qkv<LY::RB>(ldw, a.layers[l + 1].w[0], h, sp, wave, lane);
+                stage_qkv_acc<Q8>(wq, a.layers[l + 1].w[0], h, sp, wave, lane);
             }
         }
     } else if (wg - PD_NA < PD_NW) {
@@ -828,14 +711,11 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
         // mlp-proj rows after its mlp-proj, whose registers they reuse).  Loads complete in issue
         // order, so a weight load issued shortly before a poll would hold that poll back.
         PhaseW<768, Q8, RP> WP;
-        PhaseW<768, Q8, RF> WF;
         FcW<Q8> FC;
-        const bool fc_dot = a.var & 4;   // fc by v_dot2 rows (else one MFMA block)
         PhaseW<3072, Q8, RM> WM;
         LNParams lnp;
         load_phase(WP, a.layers[0].w[1], a.layers[0].s[1], a.layers[0].b[1], g * RP, wave, lane);
-        if (fc_dot) load_phase(WF, a.layers[0].w[2], a.layers[0].s[2], a.layers[0].b[2], g * RF, wave, lane);
-        else load_fc(FC, a.layers[0].w[2], a.layers[0].s[2], a.layers[0].b[2], g * RF, wave, lane);
+        load_fc(FC, a.layers[0].w[2], a.layers[0].s[2], a.layers[0].b[2], g * RF, wave, lane);
         load_ln(lnp, a.layers[0].ln2_g, a.layers[0].ln2_b);
         load_phase(WM, a.layers[0].w[3], a.layers[0].s[3], a.layers[0].b[3], g * RM, wave, lane);
         unsigned long long t_st = __builtin_amdgcn_s_memrealtime();   // this work-group's last store
@@ -859,36 +739,6 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 const uint32_t u = __float_as_uint(w);
                 return h2f((uint16_t)(hi ? u >> 16 : u & 0xffff));
             };
-            if (a.var & 1) {
-#pragma unroll
-            for (int i = 0; i < 3; ++i) {
-                const int e = tid + PD_T * i, hh = e / PD_D, d = e % PD_D;
-                const float *p = part + hh * PD_S * PD_PW;
-                float m4[PD_S], l4[PD_S], s4[PD_S], f4[PD_S], c4[PD_S];
-#pragma unroll
-                for (int s2 = 0; s2 < PD_S; ++s2) {
-                    m4[s2] = p[s2 * PD_PW + AW_M];
-                    l4[s2] = p[s2 * PD_PW + AW_L];
-                    s4[s2] = p[s2 * PD_PW + AW_S];
-                    c4[s2] = half_of(p[s2 * PD_PW + AW_C + d / 2], d & 1);   // c / l of split s2
-                }
-                const float vpos = half_of(p[(d / KS) * PD_PW + AW_V + (d % KS) / 2], d & 1);
-                const float spos = ((s4[0] + s4[1]) + (s4[2] + s4[3])) * 0.125f;
-                float mx = spos;
-#pragma unroll
-                for (int s2 = 0; s2 < PD_S; ++s2) mx = (l4[s2] != 0.f) ? fmaxf(mx, m4[s2]) : mx;
-#pragma unroll
-                for (int s2 = 0; s2 < PD_S; ++s2) f4[s2] = (l4[s2] != 0.f) ? __expf(m4[s2] - mx) * l4[s2] : 0.f;
-                float L = __expf(spos - mx);
-                float c = L * vpos;
-#pragma unroll
-                for (int s2 = 0; s2 < PD_S; ++s2) {
-                    L += f4[s2];
-                    c += c4[s2] * f4[s2];
-                }
-                xn[e] = (f16)(c / L);
-            }
-            } else {
             // The heads' weights first: lanes 0-14 of wave w form, for heads w, w + 4, w + 8, the five
             // parts' weights (four splits and the new key) normalized by the head's total, into LDS;
             // the wave's own reads of them below come after its writes (in order), so no barrier.
@@ -928,7 +778,6 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 for (int s2 = 0; s2 < PD_S; ++s2) c += half_of(p[s2 * PD_PW + AW_C + d / 2], d & 1) * hw[5 * i + s2];
                 xn[e] = (f16)c;
             }
-            }
             if (l == 1) mark(118);
             lds_barrier();
             if (l == 1) mark(119);
@@ -946,11 +795,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             mark(64 + 4 * l + 2);
             layernorm768(xn, xs, lnp, lane);
             if (l == 1) mark(120);
-            if (fc_dot) {
-                run_phase(WF, xn, wave, lane, [&](int k, float v) {
-                    if (lane == 0) hout[k] = __builtin_bit_cast(uint16_t, (f16)gelu_tanh(v));
-                });
-            } else {
+            {
                 // QS MFMAs per wave over its K range; column 0 of D (lanes 0, 16, 32, 48) holds rows
                 // 4(l / 16) .. +3; the four waves' partials are summed in wave order by threads 0-15.
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -993,8 +838,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
             if (next) {
                 const PDLayer &ln = a.layers[l + 1];
                 load_phase(WP, ln.w[1], ln.s[1], ln.b[1], g * RP, wave, lane);
-                if (fc_dot) load_phase(WF, ln.w[2], ln.s[2], ln.b[2], g * RF, wave, lane);
-                else load_fc(FC, ln.w[2], ln.s[2], ln.b[2], g * RF, wave, lane);
+                load_fc(FC, ln.w[2], ln.s[2], ln.b[2], g * RF, wave, lane);
                 load_ln(lnp, ln.ln2_g, ln.ln2_b);
             }
             run_phase(WM, hs, wave, lane, [&](int k, float v) {
@@ -1154,13 +998,10 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
 // ------------------------------------------------------------------------------ host side
 static int g_pd_spin = PD_SPIN;
 static unsigned long long *g_pd_trace = nullptr;
-static int g_pd_qa = 1;   // q/k/v GEMV on the matrix cores (1) or v_dot2 from LDS (0), for new plans
 static int g_pd_hold[3] = {-1, -1, -1};   // hold-off overrides for new plans (< 0: the constant)
-static int g_pd_var = 0;                  // measurement variant bits for new plans
 
 typedef void (*PDKernel)(PDArgs);
-static const PDKernel kPersist[2][2] = {{k_decode_persist<false, false>, k_decode_persist<false, true>},
-                                        {k_decode_persist<true, false>, k_decode_persist<true, true>}};
+static const PDKernel kPersist[2] = {k_decode_persist<false>, k_decode_persist<true>};
 
 // The step's work-groups wait on each other's words, so all PD_G of them must be resident at once:
 // the device must hold PD_G of them (one per CU with this LDS footprint) side by side.
@@ -1208,8 +1049,7 @@ bool persist_plan(PDPlan &p, const GPT2Backend *be, const GPT2WeightsGPU *w, GPT
     if (nq != 0 && nq != 4 * GPT2_N_LAYER) return false;
     if (kv->maxT > GPT2_N_CTX) return false;   // an attention wave holds at most 64 keys
     p.q8 = nq != 0;
-    p.qa = g_pd_qa != 0;
-    if (!persist_fits(kPersist[p.q8][p.qa])) return false;
+    if (!persist_fits(kPersist[p.q8])) return false;
     a.wte = w->wte;
     a.wpe = w->wpe;
     a.lnf_g = w->lnf_g;
@@ -1227,12 +1067,11 @@ bool persist_plan(PDPlan &p, const GPT2Backend *be, const GPT2WeightsGPU *w, GPT
     a.trace = g_pd_trace;
     const unsigned hold0[3] = {PD_HOLD_ATT, PD_HOLD_X, PD_HOLD_HID};
     for (int i = 0; i < 3; ++i) a.hold[i] = g_pd_hold[i] >= 0 ? (unsigned)g_pd_hold[i] : hold0[i];
-    a.var = g_pd_var;
     return true;
 }
 
 void persist_launch(const PDPlan &p, hipStream_t s) {
-    hipLaunchKernelGGL(kPersist[p.q8][p.qa], dim3(PD_G), dim3(PD_T), 0, s, p.args);
+    hipLaunchKernelGGL(kPersist[p.q8], dim3(PD_G), dim3(PD_T), 0, s, p.args);
 }
 
 size_t persist_ll_bytes() { return (size_t)LL_WORDS * 8; }
@@ -1246,14 +1085,10 @@ int persist_spin() { return g_pd_spin; }
 // that finds a word missing).  A tiny value
 // forces the timeout path with every kernel still exiting normally.
 extern "C" void gpt2_tune_decode_spin(int rounds) { g2::g_pd_spin = rounds >= 0 ? rounds : g2::PD_SPIN; }
-// Tuning / test hook: the persistent step's q/k/v GEMV for graphs created afterwards: 1 on the matrix
-// cores from accumulation registers, 0 v_dot2 over rows staged in LDS, < 0 the default (1).
-extern "C" void gpt2_tune_decode_qkv_mfma(int on) { g2::g_pd_qa = on < 0 ? 1 : (on != 0); }
 // Tuning hook: the persistent step's poll hold-offs, in 10 ns ticks, for graphs created afterwards:
-// before the attention words, x after proj, gelu(fc); a value < 0 keeps that hold-off's default.
-// Measurement hook: variant bits of the persistent step for graphs created afterwards (0: the default
-// code paths; a set bit selects the previous form of one piece, kept for interleaved A/B).
-extern "C" void gpt2_tune_decode_variant(int bits) { g2::g_pd_var = bits; }
+// before the attention words, x after proj, gelu(fc); a value < 0 keeps that hold-off's default.  The
+// defaults were measured on MI355X (interleaved A/B); a hold only delays a poll, so any value is
+// correct, and a box whose exchanges are faster or slower can re-tune them without a rebuild.
 extern "C" void gpt2_tune_decode_holds(int att, int x, int hid) {
     g2::g_pd_hold[0] = att;
     g2::g_pd_hold[1] = x;

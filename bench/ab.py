@@ -32,11 +32,8 @@ SPEC: comma-separated key=value knobs; an empty SPEC ("") is the library's defau
                  product, or the residual added in place) instead of the plain one
   m=M            gemm_shape / gemm_set: rows of A (default 512)
   skinny=N       the skinny GEMM takes M up to N (gpt2_tune_gemm_skinny; 0: never, -1: the default)
-  qkv=1|0        decode_step: the persistent step's q/k/v GEMV on the matrix cores from accumulation
-                 registers (1) or v_dot2 over rows staged in LDS (0) (gpt2_tune_decode_qkv_mfma)
   holds=A/X/H    decode_step: the persistent step's poll hold-offs in 10 ns ticks (attention words, x,
                  gelu(fc); -1 keeps a default; gpt2_tune_decode_holds)
-  var=BITS       decode_step: the persistent step's measurement variant bits (gpt2_tune_decode_variant)
 
 Examples:
   python bench/ab.py gemm_set --a "" --b gemm_cfg=12
@@ -285,8 +282,8 @@ class DecodeWorkload:
         self.env, self.cache = env, {}
         self.body = env.synth.make_body(seed=1234, plain=True)
 
-    def state(self, backend, mode, P, qkv=-1, holds=(-1, -1, -1), var=0):
-        key = (backend, mode, P, qkv, holds, var)
+    def state(self, backend, mode, P, holds=(-1, -1, -1)):
+        key = (backend, mode, P, holds)
         if key not in self.cache:
             env, pkg, L = self.env, self.env.pkg, self.env.L
             model = pkg.Model(self.body)
@@ -303,14 +300,13 @@ class DecodeWorkload:
             pkg.check("prefill")
             first = int(np.argmax(pkg.half_bits_to_f32(logits.numpy(np.uint16, (50257,)))))
             m = {"persistent": pkg.DECODE_PERSISTENT, "multi": pkg.DECODE_MULTI}[mode]
-            L.gpt2_tune_decode_qkv_mfma(qkv)
-            L.gpt2_tune_decode_holds(*holds)
-            L.gpt2_tune_decode_variant(var)
+            def tune(name, *args):          # an older build (lib=) may lack these hooks
+                if hasattr(L, name):
+                    getattr(L, name)(*args)
+            tune("gpt2_tune_decode_holds", *holds)
             g = L.gpt2_decode_graph_create_mode(be, C.byref(model.gpu), C.byref(kv.kv), C.byref(scr.s), logits.ptr,
                                                 tokens.ptr, m)
-            L.gpt2_tune_decode_qkv_mfma(-1)
-            L.gpt2_tune_decode_holds(-1, -1, -1)
-            L.gpt2_tune_decode_variant(0)
+            tune("gpt2_tune_decode_holds", -1, -1, -1)
             if not g:
                 pkg.check("graph create")
                 raise RuntimeError("graph create failed")
@@ -322,7 +318,7 @@ class DecodeWorkload:
         pos = int(knobs.get("pos", 512))
         holds = tuple(int(v) for v in knobs.get("holds", "-1/-1/-1").split("/"))
         _, _, _, g, first = self.state(knobs.get("backend", "int8"), knobs.get("mode", "persistent"), max(pos, 1),
-                                       int(knobs.get("qkv", -1)), holds, int(knobs.get("var", 0)))
+                                       holds)
         ms, out = C.c_float(), []
         for _ in range(10):
             L.gpt2_decode_graph_set(g, first, pos)

@@ -356,18 +356,14 @@ def first_argmax(lg16):
     return int(np.argmax(oracle.f16_to_f32(lg16)))
 
 
-@pytest.mark.parametrize("qkv_mfma", [1, 0])
 @pytest.mark.parametrize("backend", ["int8", "gemv"])
-def test_persistent_decode_matches_eager(pkg, L, synth, model, backend, qkv_mfma):
+def test_persistent_decode_matches_eager(pkg, L, synth, model, backend):
     """One-kernel-per-token decode against the eager multi-kernel step, teacher-forced: before every
     replay the graph state is set to the eager run's (token, pos), so each step starts from the same
     cache prefix and input token.  Gates: rel_err <= 1e-2 and KL < 2e-3 per step against the eager
-    logits; the step's own greedy token equals the first argmax of its own logits exactly.  Both forms
-    of the step's q/k/v GEMV (gpt2_tune_decode_qkv_mfma: MFMA from accumulation registers, the
-    default, and v_dot2 over rows staged in LDS)."""
+    logits; the step's own greedy token equals the first argmax of its own logits exactly."""
     if backend == "int8":
         model.quantize()
-    L.gpt2_tune_decode_qkv_mfma(qkv_mfma)
     try:
         ids = synth.token_ids(40, seed=18)
         P, n = len(ids), 20
@@ -401,7 +397,6 @@ def test_persistent_decode_matches_eager(pkg, L, synth, model, backend, qkv_mfma
         scr.free()
         kv.free()
     finally:
-        L.gpt2_tune_decode_qkv_mfma(-1)
         if backend == "int8":
             L.gpt2_quant_free(C.byref(model.q))
             model.q = None
