@@ -322,29 +322,30 @@ __device__ __forceinline__ void load_ln(LNParams &p, const uint16_t *g, const ui
     }
 }
 
+// The lane's twelve values are summed as a tree (the latency is two reductions long, not 24 adds),
+// and rstd is the hardware reciprocal square root (1 ulp).
+__device__ __forceinline__ float sum12(const float (&v)[12]) {
+    return (((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]))) + ((v[8] + v[9]) + (v[10] + v[11]));
+}
 __device__ __forceinline__ void layernorm768(f16 *xn, const f16 *xs, const LNParams &p, int lane) {
-    float v[12], s = 0.f;
+    float v[12], xe[3];
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const f16x4 x4 = *reinterpret_cast<const f16x4 *>(xs + 12 * lane + 4 * i);
 #pragma unroll
         for (int t = 0; t < 4; ++t) v[4 * i + t] = (float)x4[t];
+        xe[i] = (float)xs[threadIdx.x + PD_T * i];
     }
-#pragma unroll
-    for (int i = 0; i < 12; ++i) s += v[i];
-    const float mean = wave_sum_u(s) * (1.0f / PD_E);
-    float q = 0.f;
+    const float mean = wave_sum_u(sum12(v)) * (1.0f / PD_E);
+    float d2[12];
 #pragma unroll
     for (int i = 0; i < 12; ++i) {
         const float d = v[i] - mean;
-        q += d * d;
+        d2[i] = d * d;
     }
-    const float rstd = 1.0f / sqrtf(wave_sum_u(q) * (1.0f / PD_E) + GPT2_LN_EPS);
+    const float rstd = __builtin_amdgcn_rsqf(wave_sum_u(sum12(d2)) * (1.0f / PD_E) + GPT2_LN_EPS);
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        const int e = threadIdx.x + PD_T * i;
-        xn[e] = (f16)(((float)xs[e] - mean) * rstd * h2f(p.g[i]) + h2f(p.b[i]));
-    }
+    for (int i = 0; i < 3; ++i) xn[threadIdx.x + PD_T * i] = (f16)((xe[i] - mean) * rstd * h2f(p.g[i]) + h2f(p.b[i]));
     lds_barrier();
 }
 
@@ -592,17 +593,15 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 // Every lane computes its dot product (kr is zero past w1) and the out-of-range lanes
                 // are masked by a select afterwards: no lane-divergent branch precedes the DPP
                 // reduction, so every lane of the row holds a value the select wrote.
-                float d0 = 0.f, d1 = 0.f;
+                float dd[4] = {0.f, 0.f, 0.f, 0.f};   // four independent chains of eight
 #pragma unroll
                 for (int c = 0; c < 8; ++c)
 #pragma unroll
-                    for (int t = 0; t < 4; t += 2) {
-                        d0 = __builtin_amdgcn_fdot2(f16x2{q[c][2 * t], q[c][2 * t + 1]}, f16x2{kr[c][2 * t], kr[c][2 * t + 1]},
-                                                    d0, false);
-                        d1 = __builtin_amdgcn_fdot2(f16x2{q[c][2 * t + 2], q[c][2 * t + 3]},
-                                                    f16x2{kr[c][2 * t + 2], kr[c][2 * t + 3]}, d1, false);
-                    }
-                const float sv = on ? (d0 + d1) * 0.125f : -INFINITY;
+                    for (int t = 0; t < 4; ++t)
+                        dd[2 * (c & 1) + (t >> 1)] = __builtin_amdgcn_fdot2(f16x2{q[c][2 * t], q[c][2 * t + 1]},
+                                                                            f16x2{kr[c][2 * t], kr[c][2 * t + 1]},
+                                                                            dd[2 * (c & 1) + (t >> 1)], false);
+                const float sv = on ? ((dd[0] + dd[1]) + (dd[2] + dd[3])) * 0.125f : -INFINITY;
                 m_w = wave_max_u(sv);   // finite: key w0 is in range
                 const float pv = on ? __expf(sv - m_w) : 0.f;
                 pl[wave][(lane & 7) * 8 + (lane >> 3)] = pv;
@@ -610,10 +609,14 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 const float4 pa = *reinterpret_cast<const float4 *>(&pl[wave][slot * 8]);
                 const float4 pb = *reinterpret_cast<const float4 *>(&pl[wave][slot * 8 + 4]);
                 const float pr[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+                // keys w0 + slot + 8t: past the wave's last key p is 0, so those terms are skipped
+                const int nt = __builtin_amdgcn_readfirstlane((w1 - w0 + 7) >> 3);
 #pragma unroll
                 for (int t = 0; t < 8; ++t)
+                    if (t < nt) {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) cacc[e] += pr[t] * (float)vr[t][e];   // p = 0 past w1
+                        for (int e = 0; e < 8; ++e) cacc[e] += pr[t] * (float)vr[t][e];
+                    }
             }
 #pragma unroll
             for (int e = 0; e < 8; ++e) cl[wave][dg + e][slot] = cacc[e];
