@@ -65,19 +65,21 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-    v = row16_sum(v);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
+
+// The four row sums of row16_sum combined as (r0 + r1) + (r2 + r3), read as scalars (v_readlane)
+// instead of crossing rows through two LDS permutes (xor 16, then xor 32).  Every lane of a row holds
+// the same bits after row16_sum, so this is bit for bit what the permutes give every lane.
+__device__ __forceinline__ float cross_rows_sum(float v) {
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
+__device__ __forceinline__ float wave_sum(float v) { return cross_rows_sum(row16_sum(v)); }
 
 // Wave-uniform sum / max: DPP within each 16-lane row, then the four row results are read as
 // scalars (v_readlane) instead of crossing rows through LDS permutes.  Every lane gets the same
 // value; the row results are combined in the fixed order 0, 16, 32, 48.
-__device__ __forceinline__ float lane_f(float v, int l) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
-}
 __device__ __forceinline__ float wave_sum_u(float v) {
     v = row16_sum(v);
     return ((lane_f(v, 0) + lane_f(v, 16)) + lane_f(v, 32)) + lane_f(v, 48);
@@ -143,7 +145,7 @@ __device__ __forceinline__ void ln_row768(const f16x4 (&x)[3], const f16x4 (&g)[
 
 // ln_row768 on R rows at once (row r in x[r], lane layout as above): each row goes through exactly
 // ln_row768's operations, so the bits are those of R calls, but the rows' cross-lane sums are
-// issued together, so their latencies (each wave_sum ends in two LDS permutes) overlap instead of
+// issued together, so their latencies (DPP steps and lane reads) overlap instead of
 // running one row after another.
 template <int R>
 __device__ __forceinline__ void ln_rows768(const f16x4 (&x)[R][3], const f16x4 (&g)[3], const f16x4 (&b)[3],
@@ -162,9 +164,7 @@ __device__ __forceinline__ void ln_rows768(const f16x4 (&x)[R][3], const f16x4 (
 #pragma unroll
     for (int r = 0; r < R; ++r) s[r] = row16_sum(s[r]);
 #pragma unroll
-    for (int r = 0; r < R; ++r) s[r] += __shfl_xor(s[r], 16, 64);
-#pragma unroll
-    for (int r = 0; r < R; ++r) s[r] += __shfl_xor(s[r], 32, 64);
+    for (int r = 0; r < R; ++r) s[r] = cross_rows_sum(s[r]);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         mean[r] = s[r] / (float)GPT2_N_EMBD;
@@ -178,9 +178,7 @@ __device__ __forceinline__ void ln_rows768(const f16x4 (&x)[R][3], const f16x4 (
 #pragma unroll
     for (int r = 0; r < R; ++r) q[r] = row16_sum(q[r]);
 #pragma unroll
-    for (int r = 0; r < R; ++r) q[r] += __shfl_xor(q[r], 16, 64);
-#pragma unroll
-    for (int r = 0; r < R; ++r) q[r] += __shfl_xor(q[r], 32, 64);
+    for (int r = 0; r < R; ++r) q[r] = cross_rows_sum(q[r]);
 #pragma unroll
     for (int r = 0; r < R; ++r) rstd[r] = 1.0f / sqrtf(q[r] / (float)GPT2_N_EMBD + GPT2_LN_EPS);
 #pragma unroll

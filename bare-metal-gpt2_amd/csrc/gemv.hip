@@ -47,11 +47,16 @@ __device__ __forceinline__ float dot16q(const i32x4 w, const f16x8 x0, const f16
     return acc;
 }
 
+// The sum over the LPR lanes of a row slot: DPP within 16 lanes, then (LPR = 32, 64) the 16-lane row
+// sums read as scalars and combined in the order the xor-16 / xor-32 permutes would (same bits).
 template <int LPR>
 __device__ __forceinline__ float slot_sum(float v) {
     v = row16_sum(v);
-    if constexpr (LPR >= 32) v += __shfl_xor(v, 16, 64);
-    if constexpr (LPR >= 64) v += __shfl_xor(v, 32, 64);
+    if constexpr (LPR >= 64) return cross_rows_sum(v);
+    if constexpr (LPR == 32) {
+        const float lo = lane_f(v, 0) + lane_f(v, 16), hi = lane_f(v, 32) + lane_f(v, 48);
+        return (threadIdx.x & 32) ? hi : lo;
+    }
     return v;
 }
 
