@@ -439,6 +439,46 @@ def test_persistent_decode_deterministic_free_run(pkg, L, synth, model):
         model.gpu.q = None
 
 
+def test_persistent_decode_holds_change_timing_not_bits(pkg, L, synth, model):
+    """The poll hold-offs (gpt2_tune_decode_holds) only delay polls: graphs built with none (0 / 0 / 0),
+    the defaults and long ones (10 us each) give the same greedy tokens and the same final logits bit
+    for bit over a 12-step free run."""
+    model.quantize()
+    try:
+        ids = synth.token_ids(24, seed=23)
+        P, n = len(ids), 12
+        kv, scr, logits = decode_setup(pkg, L, model, ids, "int8")
+        first = first_argmax(logits.numpy(np.uint16, (V,)))
+        tokens = pkg.Dev(1024 * 4)
+        runs = []
+        for holds in ((-1, -1, -1), (0, 0, 0), (1000, 1000, 1000)):
+            L.gpt2_tune_decode_holds(*holds)
+            try:
+                g = L.gpt2_decode_graph_create_mode(pkg.backend("int8"), C.byref(model.gpu), C.byref(kv.kv),
+                                                    C.byref(scr.s), logits.ptr, tokens.ptr, pkg.DECODE_PERSISTENT)
+            finally:
+                L.gpt2_tune_decode_holds(-1, -1, -1)
+            assert g, pkg.check("graph create")
+            try:
+                tok, pos = C.c_int(), C.c_int()
+                assert L.gpt2_decode_graph_set(g, first, P) == 0
+                assert L.gpt2_decode_graph_run(g, n) == 0
+                assert L.gpt2_decode_graph_sync(g, C.byref(tok), C.byref(pos)) == 0, pkg.check(f"holds {holds}")
+                assert pos.value == P + n
+                runs.append((list(tokens.numpy(np.int32, (1024,))[P + 1:P + n + 1]), logits.numpy(np.uint16, (V,))))
+            finally:
+                L.gpt2_decode_graph_destroy(g)
+        for r in runs[1:]:
+            assert r[0] == runs[0][0]
+            assert np.array_equal(r[1], runs[0][1])
+        scr.free()
+        kv.free()
+    finally:
+        L.gpt2_quant_free(C.byref(model.q))
+        model.q = None
+        model.gpu.q = None
+
+
 def test_persistent_decode_positions(pkg, L, synth, model):
     """Key-split edge cases of the persistent step: position 0 (no earlier keys, every split empty),
     small contexts where some splits or waves get no keys, splits that do not divide evenly, and the
