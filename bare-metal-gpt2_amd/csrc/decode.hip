@@ -8,13 +8,13 @@
 // Design:
 //   * PD_G work-groups (one per CU) run the whole step, in four phases per layer:
 //       A  48 attention work-groups, four per head (key splits): LN1 of x, the head's q and the
-//          split's 16-row slices of k and v of the new key (96 weight rows, staged in LDS by DMA
-//          during the previous layer), the K/V append, attention over the split's share of the
-//          earlier keys; they send an unnormalized partial (m, l, c[64]) plus the slice's part of
-//          q.k_new and its v_new slice.
+//          split's 16-row slices of k and v of the new key (96 weight rows on the matrix cores, their
+//          fragments loaded into accumulation registers during the previous layer), the K/V
+//          append, attention over the split's share of the earlier keys; they send an unnormalized
+//          partial (m, l, c[64]) plus the slice's part of q.k_new and its v_new slice.
 //       P  192 GEMV work-groups: combine the partials (the new key is one more partial), proj rows,
 //          + bias + residual.
-//       F  the same work-groups: LN2, fc rows, gelu.
+//       F  the same work-groups: LN2, fc rows (one 16-row block on the matrix cores), gelu.
 //       M  the same work-groups: mlp-proj rows + bias + residual.
 //     then LN_f + tied head + argmax on every work-group, and work-group 0 picks the token.
 //   * Phases exchange their (small) output vectors through "flag words": 64-bit words holding 32 bits
@@ -25,7 +25,7 @@
 //     single-copy atomic, so data and flag arrive together.
 //   * Every phase's weights are in flight before its input arrives: GEMV rows go to registers one
 //     phase ahead (issued right after the previous poll completed, so a poll never queues behind
-//     them), the attention work-groups' q/k/v rows go to LDS a layer ahead.  Barriers between waves
+//     them), the attention work-groups' q/k/v fragments a layer ahead.  Barriers between waves
 //     wait for LDS traffic only, so they do not drain those loads; per-layer pointers come from the
 //     kernel argument segment (scalar loads) and fp16 parameters stay unconverted until used, since
 //     either would otherwise make the wave wait for every load it has in flight.
@@ -481,7 +481,7 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
     if (wg < PD_NA) {
         // ================================ attention work-group: head h, key split sp
         // Per layer: LN1 of x; the head's q and this split's slices of k and v of key `pos`, from
-        // the weight rows staged in LDS during the previous layer; the K/V append of those slices;
+        // the weight fragments loaded during the previous layer; the K/V append of those slices;
         // attention of q over the split's share of keys [0, pos); then the unnormalized partial
         // (m, l, c[64]), the slice's share of q.k_pos and the v_pos slice to the exchange.  The
         // combiner treats key `pos` as one more partial (m = q.k_pos / 8, l = 1, c = v_pos).
