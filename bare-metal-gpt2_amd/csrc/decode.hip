@@ -583,6 +583,14 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
                 Kc[(size_t)pos * PD_D + KS * sp + tid] = __builtin_bit_cast(uint16_t, qkvh[PD_D + tid]);
                 Vc[(size_t)pos * PD_D + KS * sp + tid] = __builtin_bit_cast(uint16_t, qkvh[PD_D + KS + tid]);
             }
+            // This split's part of q.k_pos (fp32 products of the fp16 values, summed over the 16-lane
+            // row): wave 3, which has the fewest keys, before its attention.
+            float *sdot = reinterpret_cast<float *>(lds + LDS_MISC + 128);
+            if (__builtin_amdgcn_readfirstlane(wave) == 3) {   // a scalar branch: the DPP sum sees every lane
+                const float pq = lane < KS ? (float)qkvh[KS * sp + lane] * (float)qkvh[PD_D + lane] : 0.f;
+                const float d = row16_sum(pq);
+                if (lane == 0) *sdot = d;
+            }
             // ---- attention over the wave's keys (one softmax pass), then the work-group merge
             float m_w = -INFINITY, l_w = 0.f;
             float cacc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -621,21 +629,13 @@ __global__ __launch_bounds__(PD_T) void k_decode_persist(PDArgs a) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) cl[wave][dg + e][slot] = cacc[e];
             // Each wave sums its eight slots of every dimension itself (lane = dimension; its own
-            // LDS writes above come first, in order), and wave 3 (the fewest keys) forms this
-            // split's part of q.k_pos, so the merge below reads one value per wave and dimension.
+            // LDS writes above come first, in order), so the merge below reads one value per wave and
+            // dimension.
             float *cs = &pl[wave][0];   // the wave's softmax scratch, free again
-            float *sdot = reinterpret_cast<float *>(lds + LDS_MISC + 128);
             {
                 const float4 ca = *reinterpret_cast<const float4 *>(&cl[wave][lane][0]);
                 const float4 cb = *reinterpret_cast<const float4 *>(&cl[wave][lane][4]);
                 cs[lane] = ((ca.x + ca.y) + (ca.z + ca.w)) + ((cb.x + cb.y) + (cb.z + cb.w));
-                if (tid == 3 * 64) {
-                    // q[KS*sp ..] . k_pos[KS*sp ..] in fp32 from the fp16 values
-                    float d = 0.f;
-#pragma unroll
-                    for (int i = 0; i < KS; ++i) d += (float)qkvh[KS * sp + i] * (float)qkvh[PD_D + i];
-                    *sdot = d;
-                }
             }
             if (lane == 0) {
                 sm[wave] = m_w;
