@@ -1069,7 +1069,8 @@ bool persist_plan(PDPlan &p, const GPT2Backend *be, const GPT2WeightsGPU *w, GPT
     a.err = err;
     a.trace = g_pd_trace;
     const unsigned hold0[3] = {PD_HOLD_ATT, PD_HOLD_X, PD_HOLD_HID};
-    for (int i = 0; i < 3; ++i) a.hold[i] = g_pd_hold[i] >= 0 ? (unsigned)g_pd_hold[i] : hold0[i];
+    // a hold only delays a poll; capped at 100 us so that no setting can stall a step for long
+    for (int i = 0; i < 3; ++i) a.hold[i] = g_pd_hold[i] >= 0 ? (unsigned)min(g_pd_hold[i], 10000) : hold0[i];
     return true;
 }
 
@@ -1089,7 +1090,8 @@ int persist_spin() { return g_pd_spin; }
 // forces the timeout path with every kernel still exiting normally.
 extern "C" void gpt2_tune_decode_spin(int rounds) { g2::g_pd_spin = rounds >= 0 ? rounds : g2::PD_SPIN; }
 // Tuning hook: the persistent step's poll hold-offs, in 10 ns ticks, for graphs created afterwards:
-// before the attention words, x after proj, gelu(fc); a value < 0 keeps that hold-off's default.  The
+// before the attention words, x after proj, gelu(fc); a value < 0 keeps that hold-off's default, and
+// values above 10000 (100 us) are taken as 10000.  The
 // defaults were measured on MI355X (interleaved A/B); a hold only delays a poll, so any value is
 // correct, and a box whose exchanges are faster or slower can re-tune them without a rebuild.
 extern "C" void gpt2_tune_decode_holds(int att, int x, int hid) {
